@@ -1,0 +1,45 @@
+"""fni8serve_amd: the W8A8 linear path of fni8-serve, native to MI355X (gfx950).
+
+Drop-in pieces for the reference's seam (fni8serve/layers/linear.py and its
+callers):
+
+    linear(x, qt, bias=None)      the `fni8.linear` call (linear.py:69)
+    QTensor                       the quantized-weight container
+    quantize_int8_rowwise(w)      load-time per-row weight quantization
+    LinearW8A8, GatedMLP, SparseMoE, LMHead and the weight helpers
+
+The arithmetic runs in libfni8amd.so (hand-written HIP kernels for gfx950,
+C ABI in include/fni8amd.h); this package is the host side.  The directory is
+named `fni8-serve_amd`; it is imported as `fni8serve_amd`.
+"""
+from .ops import (  # noqa: F401
+    gemm_w8a8,
+    gemm_w8a8_grouped,
+    linear,
+    linear_with_intermediates,
+    moe_combine,
+    moe_sort,
+    quantize_rowwise,
+)
+from .qtensor import QTensor  # noqa: F401
+from .quant import quantize_int8_rowwise  # noqa: F401
+from .layers import (  # noqa: F401
+    NF4_CODEBOOK,
+    GatedMLP,
+    LinearW8A8,
+    LMHead,
+    Qwen3MLP,
+    SparseMoE,
+    _dequant_weight,
+    gate_up_weight,
+    merge_qtensor,
+    qkv_weight,
+    to_qtensor,
+)
+
+__all__ = [
+    "linear", "linear_with_intermediates", "quantize_rowwise", "gemm_w8a8", "gemm_w8a8_grouped",
+    "moe_sort", "moe_combine", "QTensor", "quantize_int8_rowwise", "LinearW8A8", "GatedMLP",
+    "Qwen3MLP", "SparseMoE", "LMHead", "NF4_CODEBOOK", "to_qtensor", "merge_qtensor",
+    "qkv_weight", "gate_up_weight",
+]

@@ -1,0 +1,209 @@
+// extern "C" entry points: argument checks, then the launches on the caller's
+// stream.  Nothing here allocates device memory or synchronises.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "common.h"
+
+namespace fni8h {
+
+static thread_local char g_detail[512];
+
+void set_error_detail(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_detail, sizeof g_detail, fmt, ap);
+    va_end(ap);
+}
+
+}  // namespace fni8h
+
+namespace {
+
+using fni8h::set_error_detail;
+
+constexpr int64_t kMaxDim = (int64_t)1 << 31;
+constexpr int kMaxDevices = 64;
+// 0 = unknown, 1 = gfx950, -1 = other.  Written once per device; a repeated
+// write of the same value from two threads is harmless.
+int g_device_ok[kMaxDevices];
+
+int check_device() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
+        set_error_detail("no current HIP device");
+        return FNI8_ERR_DEVICE;
+    }
+    if (dev < kMaxDevices && g_device_ok[dev] == 1) return FNI8_OK;
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        set_error_detail("hipGetDeviceProperties failed on device %d", dev);
+        return FNI8_ERR_DEVICE;
+    }
+    const bool ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+    if (dev < kMaxDevices) g_device_ok[dev] = ok ? 1 : -1;
+    if (!ok) {
+        set_error_detail("device %d is %s; these kernels are built for gfx950", dev,
+                         prop.gcnArchName);
+        return FNI8_ERR_DEVICE;
+    }
+    return FNI8_OK;
+}
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+#define REQUIRE(cond, code, ...)          \
+    do {                                  \
+        if (!(cond)) {                    \
+            set_error_detail(__VA_ARGS__); \
+            return (code);                \
+        }                                 \
+    } while (0)
+
+int check_gemm_shape(int64_t M, int64_t K, int64_t N) {
+    REQUIRE(M >= 0 && M < kMaxDim, FNI8_ERR_SHAPE, "M=%lld out of range", (long long)M);
+    REQUIRE(N > 0 && N < kMaxDim, FNI8_ERR_SHAPE, "N=%lld out of range", (long long)N);
+    REQUIRE(K > 0 && K < kMaxDim, FNI8_ERR_SHAPE, "K=%lld out of range", (long long)K);
+    REQUIRE(K % 4 == 0, FNI8_ERR_SHAPE, "K=%lld is not a multiple of 4", (long long)K);
+    return FNI8_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* fni8_strerror(int code) {
+    switch (code) {
+        case FNI8_OK: return "ok";
+        case FNI8_ERR_NULL: return "required pointer is NULL";
+        case FNI8_ERR_SHAPE: return "shape out of range";
+        case FNI8_ERR_ALIGN: return "pointer or stride misaligned";
+        case FNI8_ERR_STRIDE: return "leading dimension smaller than the row";
+        case FNI8_ERR_LAUNCH: return "HIP launch error";
+        case FNI8_ERR_DEVICE: return "unsupported or missing device";
+        default: return "unknown error";
+    }
+}
+
+const char* fni8_last_error(void) { return fni8h::g_detail; }
+
+const char* fni8_version(void) { return "fni8amd 0.1.0 gfx950"; }
+
+int fni8_quantize_rowwise_f16(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* xq,
+                              int64_t ldq, float* xs, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(x && xq && xs, FNI8_ERR_NULL, "x, xq and xs are required");
+    REQUIRE(M >= 0 && M < kMaxDim, FNI8_ERR_SHAPE, "M=%lld out of range", (long long)M);
+    REQUIRE(K > 0 && K < kMaxDim && K % 4 == 0, FNI8_ERR_SHAPE,
+            "K=%lld must be positive and a multiple of 4", (long long)K);
+    REQUIRE(ldx >= K && ldq >= K, FNI8_ERR_STRIDE, "ldx=%lld ldq=%lld < K=%lld",
+            (long long)ldx, (long long)ldq, (long long)K);
+    REQUIRE(aligned(x, 2) && aligned(xs, 4), FNI8_ERR_ALIGN, "x or xs misaligned");
+    int rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_quant_rowwise((const uint16_t*)x, M, K, ldx, xq, ldq, xs,
+                                       (hipStream_t)stream);
+}
+
+int fni8_gemm_w8a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                   const int8_t* w, const float* ws, int64_t N, const void* bias, void* y,
+                   int64_t ldy, int32_t* acc_out, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(xq && xs && w && ws && y, FNI8_ERR_NULL, "xq, xs, w, ws and y are required");
+    int rc = check_gemm_shape(M, K, N);
+    if (rc) return rc;
+    REQUIRE(ldq >= K && ldy >= N, FNI8_ERR_STRIDE, "ldq=%lld < K or ldy=%lld < N",
+            (long long)ldq, (long long)ldy);
+    REQUIRE(ldq % 4 == 0 && aligned(xq, 4) && aligned(w, 4), FNI8_ERR_ALIGN,
+            "int8 operands need 4-byte aligned rows");
+    REQUIRE(aligned(xs, 4) && aligned(ws, 4) && aligned(y, 2) && aligned(bias, 2) &&
+                aligned(acc_out, 4),
+            FNI8_ERR_ALIGN, "scale/output pointers misaligned");
+    rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_gemm(xq, ldq, xs, nullptr, M, K, w, ws, N, 0, nullptr,
+                              (const uint16_t*)bias, (uint16_t*)y, ldy, acc_out,
+                              (hipStream_t)stream);
+}
+
+int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                         const float* ws, int64_t N, const void* bias, void* y, int64_t ldy,
+                         int8_t* xq, float* xs, int32_t* acc_out, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(x && w && ws && y && xq && xs, FNI8_ERR_NULL,
+            "x, w, ws, y, xq and xs are required");
+    int rc = check_gemm_shape(M, K, N);
+    if (rc) return rc;
+    REQUIRE(ldx >= K && ldy >= N, FNI8_ERR_STRIDE, "ldx=%lld < K or ldy=%lld < N",
+            (long long)ldx, (long long)ldy);
+    REQUIRE(aligned(x, 2) && aligned(xq, 4) && aligned(w, 4), FNI8_ERR_ALIGN,
+            "x, xq or w misaligned");
+    REQUIRE(aligned(xs, 4) && aligned(ws, 4) && aligned(y, 2) && aligned(bias, 2) &&
+                aligned(acc_out, 4),
+            FNI8_ERR_ALIGN, "scale/output pointers misaligned");
+    rc = check_device();
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    rc = fni8h::launch_quant_rowwise((const uint16_t*)x, M, K, ldx, xq, K, xs, st);
+    if (rc) return rc;
+    return fni8h::launch_gemm(xq, K, xs, nullptr, M, K, w, ws, N, 0, nullptr,
+                              (const uint16_t*)bias, (uint16_t*)y, ldy, acc_out, st);
+}
+
+int fni8_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E, int32_t* seg_off,
+                  int32_t* row_token, int32_t* pos, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(topi && seg_off && row_token && pos, FNI8_ERR_NULL,
+            "topi, seg_off, row_token and pos are required");
+    REQUIRE(T >= 0 && k > 0 && k <= 32 && E > 0 && E < 65536 && T * k < kMaxDim,
+            FNI8_ERR_SHAPE, "T=%lld k=%lld E=%lld out of range (k <= 32)", (long long)T,
+            (long long)k, (long long)E);
+    REQUIRE(aligned(topi, 4) && aligned(seg_off, 4) && aligned(row_token, 4) && aligned(pos, 4),
+            FNI8_ERR_ALIGN, "int32 arrays misaligned");
+    int rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_moe_sort(topi, T, k, E, seg_off, row_token, pos, (hipStream_t)stream);
+}
+
+int fni8_gemm_w8a8_grouped(const int8_t* aq, const float* as, const int32_t* row_index,
+                           int64_t R_max, int64_t K, const int8_t* w, const float* ws,
+                           int64_t E, int64_t N, const int32_t* seg_off, const void* bias,
+                           void* y, int32_t* acc_out, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(aq && as && w && ws && seg_off && y, FNI8_ERR_NULL,
+            "aq, as, w, ws, seg_off and y are required");
+    int rc = check_gemm_shape(R_max, K, N);
+    if (rc) return rc;
+    REQUIRE(E > 0 && E < 65536, FNI8_ERR_SHAPE, "E=%lld out of range", (long long)E);
+    REQUIRE(aligned(aq, 4) && aligned(w, 4) && aligned(as, 4) && aligned(ws, 4) &&
+                aligned(row_index, 4) && aligned(seg_off, 4) && aligned(y, 2) &&
+                aligned(bias, 2) && aligned(acc_out, 4),
+            FNI8_ERR_ALIGN, "grouped operands misaligned");
+    rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_gemm(aq, K, as, row_index, R_max, K, w, ws, N, E, seg_off,
+                              (const uint16_t*)bias, (uint16_t*)y, N, acc_out,
+                              (hipStream_t)stream);
+}
+
+int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
+                         const void* topw, const int32_t* pos, int64_t T, int64_t k,
+                         void* out, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(y_sorted && topi && topw && pos && out, FNI8_ERR_NULL,
+            "y_sorted, topi, topw, pos and out are required");
+    REQUIRE(H > 0 && H < kMaxDim && T >= 0 && T < kMaxDim && k > 0 && k <= 32 &&
+                T * k < kMaxDim,
+            FNI8_ERR_SHAPE, "H=%lld T=%lld k=%lld out of range (k <= 32)", (long long)H,
+            (long long)T, (long long)k);
+    REQUIRE(aligned(y_sorted, 2) && aligned(topw, 2) && aligned(out, 2) && aligned(topi, 4) &&
+                aligned(pos, 4),
+            FNI8_ERR_ALIGN, "combine operands misaligned");
+    int rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_moe_combine((const uint16_t*)y_sorted, H, topi, (const uint16_t*)topw,
+                                     pos, T, k, (uint16_t*)out, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,148 @@
+"""Sparse MoE FFN with the expert loop replaced by grouped W8A8 GEMMs.
+
+Same constructor and routing as fni8serve/models/moe.py:25-113 (softmax or
+sigmoid scoring, optional group-limited top-k, renormalisation, routed
+scaling, optional shared expert).  The reference then loops over experts in
+Python, with two host syncs per expert (moe.py:218-224); its docstring names
+the grouped GEMM as the intended kernel (moe.py:9-11).  On the GPU this module
+runs instead, with no host sync:
+
+    moe_sort          stable counting sort of (token, slot) by expert
+    quantize_rowwise  x quantized once per token (row-local, so every expert
+                      reuses the same int8 row)
+    grouped gate_up   one launch over all expert segments, rows gathered by token
+    act_and_mul       on the sorted rows
+    quantize_rowwise  per sorted row
+    grouped down      one launch
+    moe_combine       weighted fp16 sum in ascending expert id (index_add_ order)
+
+Because quantization is row-local and the GEMM is exact, every int8 row, int32
+accumulator and fp16 expert output equals what the per-expert loop computes.
+CPU inputs run the reference's loop unchanged.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .. import ops
+from ..qtensor import QTensor
+from .mlp import GatedMLP, get_act_and_mul
+
+
+class SparseMoE(nn.Module):
+    def __init__(self, *, gate: torch.Tensor, experts: list[tuple[QTensor, QTensor]], top_k: int,
+                 norm_topk_prob: bool = True, act: str = "silu",
+                 shared_expert: tuple[QTensor, QTensor] | None = None,
+                 shared_expert_gate: torch.Tensor | None = None, scoring_func: str = "softmax",
+                 e_score_correction_bias: torch.Tensor | None = None,
+                 routed_scaling_factor: float = 1.0, num_expert_groups: int | None = None,
+                 topk_group: int | None = None):
+        super().__init__()
+        self.gate = nn.Parameter(gate)
+        self.top_k = top_k
+        self.norm_topk_prob = norm_topk_prob
+        self.scoring_func = scoring_func
+        self.routed_scaling_factor = routed_scaling_factor
+        self.num_expert_groups = num_expert_groups
+        self.topk_group = topk_group
+        self.register_buffer(
+            "e_score_bias",
+            e_score_correction_bias.float() if e_score_correction_bias is not None else None,
+            persistent=False)
+        self.num_experts = len(experts)
+        # Stacked expert weights [E, N, K] / scales [E, N] for the grouped kernel;
+        # the per-expert modules keep views into the same storage.
+        gu = [e[0] for e in experts]
+        dn = [e[1] for e in experts]
+        for q in gu + dn:
+            if q.scheme != "per_row_i8":
+                raise ValueError(f"grouped expert GEMM needs per_row_i8 weights, got {q.scheme!r}")
+        self.register_buffer("w_gate_up", torch.stack([q.data for q in gu]).contiguous(),
+                             persistent=False)
+        self.register_buffer("s_gate_up",
+                             torch.stack([q.scale.reshape(-1).float() for q in gu]).contiguous(),
+                             persistent=False)
+        self.register_buffer("w_down", torch.stack([q.data for q in dn]).contiguous(),
+                             persistent=False)
+        self.register_buffer("s_down",
+                             torch.stack([q.scale.reshape(-1).float() for q in dn]).contiguous(),
+                             persistent=False)
+        self.experts = nn.ModuleList([
+            GatedMLP(QTensor(self.w_gate_up[e], self.s_gate_up[e], scheme="per_row_i8"),
+                     QTensor(self.w_down[e], self.s_down[e], scheme="per_row_i8"), act=act)
+            for e in range(self.num_experts)])
+        self.act_fn = get_act_and_mul(act)
+        self.shared = GatedMLP(*shared_expert, act=act) if shared_expert else None
+        self.shared_gate = (nn.Parameter(shared_expert_gate)
+                            if shared_expert_gate is not None else None)
+
+    def route(self, xf: torch.Tensor):
+        """Router (moe.py:184-214): returns (topw in x.dtype [T, k], topi [T, k])."""
+        router_logits = F.linear(xf.float(), self.gate.float())
+        if self.scoring_func == "sigmoid":
+            scores = torch.sigmoid(router_logits)
+            sel = scores + self.e_score_bias if self.e_score_bias is not None else scores
+        else:
+            scores = F.softmax(router_logits, dim=-1)
+            sel = scores
+        if self.num_expert_groups is not None and self.topk_group is not None:
+            T = xf.shape[0]
+            per_group = sel.shape[-1] // self.num_expert_groups
+            group_scores = sel.view(T, self.num_expert_groups, per_group).amax(dim=-1)
+            selected = group_scores.topk(self.topk_group, dim=-1)[1]
+            offsets = torch.arange(per_group, device=sel.device).view(1, 1, per_group)
+            expert_idx = (selected.unsqueeze(-1) * per_group + offsets).reshape(T, -1)
+            mask = torch.full_like(sel, float("-inf"))
+            mask.scatter_(1, expert_idx, 0.0)
+            sel = sel + mask
+        if self.scoring_func == "sigmoid":
+            _, topi = torch.topk(sel, self.top_k, dim=-1)
+            topw = scores.gather(-1, topi)
+        else:
+            topw, topi = torch.topk(sel, self.top_k, dim=-1)
+        if self.norm_topk_prob:
+            topw = topw / topw.sum(dim=-1, keepdim=True).clamp_min(1e-9)
+        return (topw * self.routed_scaling_factor).to(xf.dtype), topi
+
+    def experts_grouped(self, xf: torch.Tensor, topw: torch.Tensor, topi: torch.Tensor):
+        """All routed experts in two grouped launches; returns out [T, H]."""
+        T = xf.shape[0]
+        R = T * self.top_k
+        seg_off, row_token, pos = ops.moe_sort(topi, self.num_experts)
+        xq, xs = ops.quantize_rowwise(xf)
+        h = ops.gemm_w8a8_grouped(xq, xs, self.w_gate_up, self.s_gate_up, seg_off, R,
+                                  row_index=row_token)
+        a = self.act_fn(h)
+        aq, as_ = ops.quantize_rowwise(a)
+        y = ops.gemm_w8a8_grouped(aq, as_, self.w_down, self.s_down, seg_off, R)
+        return ops.moe_combine(y, topi, topw, pos)
+
+    def _experts_loop(self, xf: torch.Tensor, topw: torch.Tensor, topi: torch.Tensor):
+        """The reference's per-expert loop (moe.py:216-224), for CPU inputs."""
+        out = torch.zeros_like(xf)
+        for e in range(self.num_experts):
+            mask = topi == e
+            if not mask.any():
+                continue
+            tok_idx, slot = mask.nonzero(as_tuple=True)
+            contrib = self.experts[e](xf[tok_idx].unsqueeze(1)).squeeze(1)
+            out.index_add_(0, tok_idx, contrib * topw[tok_idx, slot].unsqueeze(-1))
+        return out
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        B, S, H = x.shape
+        xf = x.reshape(-1, H)
+        topw, topi = self.route(xf)
+        if xf.is_cuda:
+            out = self.experts_grouped(xf, topw, topi)
+        else:
+            out = self._experts_loop(xf, topw, topi)
+        if self.shared is not None:
+            shared_out = self.shared(x).reshape(-1, H)
+            if self.shared_gate is not None:
+                g = torch.sigmoid(F.linear(xf.float(), self.shared_gate.float())).to(x.dtype)
+                shared_out = shared_out * g
+            out = out + shared_out
+        return out.reshape(B, S, H)

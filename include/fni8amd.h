@@ -1,0 +1,149 @@
+/*
+ * fni8amd: C ABI of the MI355X (gfx950) W8A8 linear kernels.
+ *
+ * The reference (Josephur/fni8-serve) reaches its int8 arithmetic through the
+ * Python call `fni8.linear(x, qt, bias=...)` at fni8serve/layers/linear.py:69;
+ * `fni8` is a closed CUDA wheel (v0.1.0-rc2) with no C interface of its own.
+ * These entry points are what a binding of that call needs: plain device
+ * pointers, sizes and a stream, no framework types.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers on the current HIP device; `stream` is a
+ *     hipStream_t (NULL = the legacy default stream).  Work is enqueued on
+ *     `stream`; nothing synchronises the host.
+ *   - The library allocates no device memory and holds no mutable global
+ *     state; every buffer comes from the caller, so calls can be captured in
+ *     a HIP graph.  Calls are reentrant.
+ *   - fp16 tensors are IEEE binary16 passed as `void*` / `uint16_t*`.
+ *   - Weights follow the per_row_i8 QTensor layout (models/weights.py:18-25):
+ *     data int8 [N, K] row-major (K contiguous), scale fp32 [N].
+ *   - Arithmetic: per-token quantization s = max(amax, 1e-6) / 127 in fp32,
+ *     q = clamp(rint(x / s), -127, 127) with correctly rounded division and
+ *     ties to even; exact int32 accumulation; epilogue
+ *     y = fp16(((float)acc * s_x[m]) * s_w[n] (+ bias[n])) with one rounding
+ *     per operation.
+ *   - Return 0 on success, a negative FNI8_ERR_* code otherwise.  Argument
+ *     errors are detected before anything is launched.
+ */
+#ifndef FNI8AMD_H
+#define FNI8AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    FNI8_OK = 0,
+    FNI8_ERR_NULL = -1,      /* a required pointer is NULL */
+    FNI8_ERR_SHAPE = -2,     /* M, N, K, E, T or k out of range; K % 4 != 0 */
+    FNI8_ERR_ALIGN = -3,     /* a pointer or stride breaks the alignment rule */
+    FNI8_ERR_STRIDE = -4,    /* a leading dimension is smaller than the row */
+    FNI8_ERR_LAUNCH = -5,    /* the HIP runtime reported an error */
+    FNI8_ERR_DEVICE = -6     /* the current device is not gfx950 */
+};
+
+/* Human-readable text for an FNI8_ERR_* code. */
+const char* fni8_strerror(int code);
+
+/* Detail of the last error raised on the calling thread ("" if none). */
+const char* fni8_last_error(void);
+
+/* Library version string. */
+const char* fni8_version(void);
+
+/*
+ * Per-token symmetric activation quantization: step 1 of `fni8.linear`
+ * (replaces the quantize half of fni8.linear, fni8serve/layers/linear.py:69;
+ * semantics linear.py:5-10).
+ *   x   fp16 [M, K], row stride ldx elements (ldx >= K)
+ *   xq  int8 [M, K], row stride ldq bytes (ldq >= K)
+ *   xs  fp32 [M]: the per-row scale
+ * K must be a multiple of 4 (the reference's quantizable-linear rule,
+ * fni8serve/convert.py:128).
+ */
+int fni8_quantize_rowwise_f16(const void* x, int64_t M, int64_t K, int64_t ldx,
+                              int8_t* xq, int64_t ldq, float* xs, void* stream);
+
+/*
+ * int8 x int8 -> int32 GEMM with the fused dequant epilogue: `gemm_w8a8`
+ * (replaces the GEMM half of fni8.linear for per_row_i8 weights,
+ * fni8serve/layers/linear.py:9 and :69).
+ *   xq      int8 [M, K], row stride ldq bytes; xs fp32 [M]
+ *   w       int8 [N, K] (row stride K); ws fp32 [N]
+ *   bias    fp16 [N] or NULL
+ *   y       fp16 [M, N], row stride ldy elements
+ *   acc_out int32 [M, N] (row stride N) or NULL: the raw accumulators, for
+ *           parity checks
+ */
+int fni8_gemm_w8a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                   const int8_t* w, const float* ws, int64_t N, const void* bias, void* y,
+                   int64_t ldy, int32_t* acc_out, void* stream);
+
+/*
+ * The whole W8A8 linear, `fni8.linear(x, qt, bias)` for a per_row_i8 QTensor
+ * (replaces fni8serve/layers/linear.py:69): quantize x per token, int8 GEMM
+ * against w, dequant epilogue to fp16.
+ *   x    fp16 [M, K], row stride ldx elements (covers the non-contiguous
+ *        `hidden[:, -1]` input of fni8serve/layers/embedding.py:49-53)
+ *   xq   int8 [M, K] and xs fp32 [M]: caller-provided buffers that receive the
+ *        quantized activations and their scales
+ *   y    fp16 [M, N], row stride ldy elements; acc_out as in fni8_gemm_w8a8
+ */
+int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                         const float* ws, int64_t N, const void* bias, void* y, int64_t ldy,
+                         int8_t* xq, float* xs, int32_t* acc_out, void* stream);
+
+/*
+ * Routing sort for the grouped expert GEMM (replaces the per-expert
+ * `mask = topi == e; mask.nonzero()` gathers of SparseMoE.forward,
+ * fni8serve/models/moe.py:218-222).  A stable counting sort of the T*k
+ * (token, slot) pairs by expert id: inside each expert's segment the rows are
+ * in ascending token, then slot, order, as nonzero() returns them.
+ *   topi       int32 [T, k] expert ids in [0, E)
+ *   seg_off    int32 [E + 1]: segment offsets, seg_off[E] = T*k
+ *   row_token  int32 [T*k]: token of each sorted row
+ *   pos        int32 [T, k]: sorted row of each (token, slot)
+ * Expert ids outside [0, E) are not detected on the device; they are skipped.
+ */
+int fni8_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E, int32_t* seg_off,
+                  int32_t* row_token, int32_t* pos, void* stream);
+
+/*
+ * Grouped W8A8 GEMM over expert segments: all experts' `gemm_w8a8` calls of
+ * one projection in one launch (replaces the expert loop's linears,
+ * fni8serve/models/moe.py:223 via layers/mlp.py:39-40; the reference notes
+ * the kernel as future work at moe.py:9-11).
+ *   aq, as     int8 [rows, K] (row stride K) and fp32 [rows]: quantized
+ *              activations
+ *   row_index  int32 [R] or NULL: sorted row r reads activation row
+ *              row_index[r] (the token gather); NULL reads row r
+ *   w, ws      int8 [E, N, K] and fp32 [E, N]: stacked expert weights
+ *   seg_off    int32 [E + 1] from fni8_moe_sort; R = seg_off[E] on the device,
+ *              R_max bounds it (the launch is sized from R_max)
+ *   bias       fp16 [E, N] or NULL
+ *   y          fp16 [R_max, N] (rows >= R are not written); acc_out int32 [R_max, N] or NULL
+ */
+int fni8_gemm_w8a8_grouped(const int8_t* aq, const float* as, const int32_t* row_index,
+                           int64_t R_max, int64_t K, const int8_t* w, const float* ws,
+                           int64_t E, int64_t N, const int32_t* seg_off, const void* bias,
+                           void* y, int32_t* acc_out, void* stream);
+
+/*
+ * Weighted combine of expert outputs (replaces moe.py:224's
+ * `out.index_add_(0, tok_idx, contrib * topw[tok_idx, slot])` over the
+ * expert loop): out[t] = sum over the token's slots, in ascending expert id,
+ * of fp16(y_sorted[pos[t, j]] * topw[t, j]), accumulated from +0 in fp16.
+ *   y_sorted  fp16 [T*k, H]; topi int32 [T, k]; topw fp16 [T, k]; pos int32 [T, k]
+ *   out       fp16 [T, H]
+ */
+int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
+                         const void* topw, const int32_t* pos, int64_t T, int64_t k,
+                         void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FNI8AMD_H */

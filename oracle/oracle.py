@@ -1,0 +1,181 @@
+"""numpy front end of the C oracle (oracle/w8a8_oracle.c).
+
+TEST INFRASTRUCTURE ONLY.  Every function takes and returns numpy arrays on
+the host; fp16 arrays are `np.float16` (their bit patterns are what the C code
+reads).  Reference citations for each step live beside the C functions.
+
+parity pinning (how each function is checked, in tests/test_oracle.py):
+  f32_to_f16 / f16_to_f32 -- all 65536 fp16 bit patterns round-trip; f32->f16
+      agrees bit-for-bit with numpy's IEEE conversion on 2^24 patterns spanning
+      every exponent, ties, subnormals, overflow.
+  quant_rowwise_f16 -- hand-computed known answers (ties to even, clamp, zero
+      row, outlier), invariants (max element -> +-127, sign symmetry,
+      monotonicity, |x - q s| <= s/2), exhaustive sweep of all finite fp16
+      values, row locality.
+  gemm_i8 -- exact against float64 BLAS matmul (exact while K*127^2 < 2^53) and
+      torch._int_mm.
+  dequant_f16 -- fp64 closed form within one fp16 rounding; transposed scale
+      indexing fails the check.
+  moe_sort / grouped_w8a8_f16 / moe_combine_f16 -- brute force against the
+      reference's per-expert loop restated with `nonzero` in numpy (moe.py:218-224).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(_HERE, "_build", "liboracle_w8a8.so")
+QUANT_EPS = np.float32(1e-6)
+
+_lib = None
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(_SO):
+        subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    lib = ctypes.CDLL(_SO)
+    P, I = ctypes.c_void_p, ctypes.c_int64
+    lib.oracle_f32_to_f16.restype = ctypes.c_uint16
+    lib.oracle_f32_to_f16.argtypes = [ctypes.c_float]
+    lib.oracle_f16_to_f32.restype = ctypes.c_float
+    lib.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+    lib.oracle_f16_to_f32_n.argtypes = [P, P, I]
+    lib.oracle_f32_to_f16_n.argtypes = [P, P, I]
+    lib.oracle_quant_rowwise_f16.argtypes = [P, I, I, I, P, I, P]
+    lib.oracle_gemm_i8.argtypes = [P, I, I, I, P, I, I, P, I]
+    lib.oracle_dequant_f16.argtypes = [P, I, I, I, P, P, P, P, I]
+    lib.oracle_linear_w8a8_f16.argtypes = [P, I, I, I, P, P, I, P, P, I, P, P, P]
+    lib.oracle_moe_sort.restype = ctypes.c_int
+    lib.oracle_moe_sort.argtypes = [P, I, I, I, P, P, P, P]
+    lib.oracle_grouped_w8a8_f16.argtypes = [P, P, I, P, P, P, I, I, P, P, P, P]
+    lib.oracle_moe_combine_f16.argtypes = [P, I, P, P, P, I, I, P]
+    for fn in ("oracle_f16_to_f32_n", "oracle_f32_to_f16_n", "oracle_quant_rowwise_f16",
+               "oracle_gemm_i8", "oracle_dequant_f16", "oracle_linear_w8a8_f16",
+               "oracle_grouped_w8a8_f16", "oracle_moe_combine_f16"):
+        getattr(lib, fn).restype = None
+    _lib = lib
+    return lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dtype):
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+def f32_to_f16(f: np.ndarray) -> np.ndarray:
+    f = _c(f, np.float32)
+    out = np.empty(f.shape, np.uint16)
+    _load().oracle_f32_to_f16_n(_p(f), _p(out), f.size)
+    return out.view(np.float16)
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = _c(np.asarray(h).view(np.uint16) if np.asarray(h).dtype == np.float16 else h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    _load().oracle_f16_to_f32_n(_p(h), _p(out), h.size)
+    return out
+
+
+def quant_rowwise_f16(x: np.ndarray):
+    """x fp16 [M, K] -> (q int8 [M, K], s fp32 [M])."""
+    x = _c(x, np.float16)
+    M, K = x.shape
+    q = np.empty((M, K), np.int8)
+    s = np.empty((M,), np.float32)
+    _load().oracle_quant_rowwise_f16(_p(x), M, K, K, _p(q), K, _p(s))
+    return q, s
+
+
+def gemm_i8(a: np.ndarray, w: np.ndarray) -> np.ndarray:
+    """a int8 [M, K], w int8 [N, K] -> acc int32 [M, N]."""
+    a = _c(a, np.int8)
+    w = _c(w, np.int8)
+    M, K = a.shape
+    N = w.shape[0]
+    assert w.shape[1] == K
+    acc = np.empty((M, N), np.int32)
+    _load().oracle_gemm_i8(_p(a), K, M, K, _p(w), K, N, _p(acc), N)
+    return acc
+
+
+def dequant_f16(acc, a_s, w_s, bias=None) -> np.ndarray:
+    acc = _c(acc, np.int32)
+    M, N = acc.shape
+    a_s = _c(a_s, np.float32)
+    w_s = _c(w_s, np.float32)
+    b = None if bias is None else _c(bias, np.float16)
+    y = np.empty((M, N), np.float16)
+    _load().oracle_dequant_f16(_p(acc), N, M, N, _p(a_s), _p(w_s), _p(b), _p(y), N)
+    return y
+
+
+def linear_w8a8_f16(x, w, w_s, bias=None):
+    """Whole W8A8 linear.  Returns (y fp16 [M, N], xq int8, xs fp32, acc int32)."""
+    x = _c(x, np.float16)
+    w = _c(w, np.int8)
+    w_s = _c(w_s, np.float32)
+    b = None if bias is None else _c(bias, np.float16)
+    M, K = x.shape
+    N = w.shape[0]
+    y = np.empty((M, N), np.float16)
+    xq = np.empty((M, K), np.int8)
+    xs = np.empty((M,), np.float32)
+    acc = np.empty((M, N), np.int32)
+    _load().oracle_linear_w8a8_f16(_p(x), K, M, K, _p(w), _p(w_s), N, _p(b), _p(y), N,
+                                   _p(xq), _p(xs), _p(acc))
+    return y, xq, xs, acc
+
+
+def moe_sort(topi: np.ndarray, E: int):
+    """topi int [T, k] -> (seg_off [E+1], row_token [R], row_slot [R], pos [T, k])."""
+    topi = _c(topi, np.int32)
+    T, k = topi.shape
+    seg = np.empty((E + 1,), np.int32)
+    rt = np.empty((T * k,), np.int32)
+    rs = np.empty((T * k,), np.int32)
+    pos = np.empty((T, k), np.int32)
+    rc = _load().oracle_moe_sort(_p(topi), T, k, E, _p(seg), _p(rt), _p(rs), _p(pos))
+    if rc != 0:
+        raise ValueError("expert id out of range")
+    return seg, rt, rs, pos
+
+
+def grouped_w8a8_f16(aq, a_s, w, w_s, seg_off, row_index=None, bias=None, want_acc=False):
+    """aq int8 [rows, K], a_s fp32 [rows]; w int8 [E, N, K]; w_s fp32 [E, N];
+    seg_off [E+1]; row_index [R] (gather) or None -> y fp16 [R, N] (, acc int32)."""
+    aq = _c(aq, np.int8)
+    a_s = _c(a_s, np.float32)
+    w = _c(w, np.int8)
+    w_s = _c(w_s, np.float32)
+    seg_off = _c(seg_off, np.int32)
+    E, N, K = w.shape
+    R = int(seg_off[-1])
+    ri = None if row_index is None else _c(row_index, np.int32)
+    b = None if bias is None else _c(bias, np.float16)
+    y = np.zeros((R, N), np.float16)
+    acc = np.zeros((R, N), np.int32) if want_acc else None
+    _load().oracle_grouped_w8a8_f16(_p(aq), _p(a_s), K, _p(ri), _p(w), _p(w_s), E, N,
+                                    _p(seg_off), _p(b), _p(y), _p(acc))
+    return (y, acc) if want_acc else y
+
+
+def moe_combine_f16(y_sorted, topi, topw, pos):
+    y_sorted = _c(y_sorted, np.float16)
+    topi = _c(topi, np.int32)
+    topw = _c(topw, np.float16)
+    pos = _c(pos, np.int32)
+    T, k = topi.shape
+    H = y_sorted.shape[1]
+    out = np.empty((T, H), np.float16)
+    _load().oracle_moe_combine_f16(_p(y_sorted), H, _p(topi), _p(topw), _p(pos), T, k, _p(out))
+    return out

@@ -1,0 +1,145 @@
+"""GPU parity of the grouped (MoE) path: routing sort, grouped W8A8 GEMMs and the
+weighted combine, against the oracle and against the per-expert loop it replaces
+(fni8serve/models/moe.py:216-224)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle
+from oracle.reference_cpu import reference_moe_loop
+
+pytestmark = pytest.mark.gpu
+
+
+def _routing(wl, T, E, k, seed):
+    logits = wl.router_logits(T, E, seed=seed)
+    topw, topi = wl.route(logits, k)
+    return topw, topi
+
+
+@pytest.mark.parametrize("T", [1, 16, 256, 4096])
+def test_moe_sort_matches_oracle(pkg, wl, cuda, T):
+    E, k = wl.MOE["experts"], wl.MOE["top_k"]
+    _, topi = _routing(wl, T, E, k, seed=T)
+    seg, rt, pos = pkg.moe_sort(topi.cuda(), E)
+    torch.cuda.synchronize()
+    seg_r, rt_r, _, pos_r = oracle.moe_sort(topi.numpy(), E)
+    assert np.array_equal(seg.cpu().numpy(), seg_r)
+    assert np.array_equal(rt.cpu().numpy(), rt_r)
+    assert np.array_equal(pos.cpu().numpy(), pos_r)
+
+
+def test_moe_sort_skewed_and_empty_experts(pkg, cuda):
+    E, T, k = 64, 300, 4
+    g = torch.Generator().manual_seed(5)
+    # most tokens on experts 0-3, many experts empty, every row's ids distinct
+    topi = torch.stack([torch.randperm(6, generator=g)[:k] for _ in range(T)])
+    topi[::7] = torch.tensor([60, 61, 62, 63])
+    seg, rt, pos = pkg.moe_sort(topi.cuda(), E)
+    seg_r, rt_r, _, pos_r = oracle.moe_sort(topi.numpy(), E)
+    assert np.array_equal(seg.cpu().numpy(), seg_r)
+    assert np.array_equal(rt.cpu().numpy(), rt_r)
+    assert np.array_equal(pos.cpu().numpy(), pos_r)
+
+
+@pytest.mark.parametrize("T", [16, 256, 4096])
+@pytest.mark.parametrize("proj", ["gate_up", "down"])
+def test_grouped_gemm_bitexact(pkg, wl, cuda, T, proj):
+    E, k, H, I = (wl.MOE[n] for n in ("experts", "top_k", "hidden", "inter"))
+    N, K = (2 * I, H) if proj == "gate_up" else (H, I)
+    _, topi = _routing(wl, T, E, k, seed=T + 1)
+    w, ws = wl.expert_weights(E, N, K, seed=3 if proj == "gate_up" else 4)
+    seg, rt, _ = pkg.moe_sort(topi.cuda(), E)
+    R = T * k
+    if proj == "gate_up":  # token rows, gathered by row_token
+        x = wl.activations(T, K, seed=T + 2)
+        aq, as_ = pkg.quantize_rowwise(x.cuda())
+        y, acc = pkg.gemm_w8a8_grouped(aq, as_, w.cuda(), ws.cuda(), seg, R, row_index=rt,
+                                       want_acc=True)
+    else:                  # already-sorted rows
+        x = wl.activations(R, K, seed=T + 2)
+        aq, as_ = pkg.quantize_rowwise(x.cuda())
+        y, acc = pkg.gemm_w8a8_grouped(aq, as_, w.cuda(), ws.cuda(), seg, R, want_acc=True)
+    torch.cuda.synchronize()
+    seg_r, rt_r, _, _ = oracle.moe_sort(topi.numpy(), E)
+    aq_r, as_r = oracle.quant_rowwise_f16(x.numpy())
+    assert np.array_equal(aq.cpu().numpy(), aq_r)
+    ri = rt_r if proj == "gate_up" else None
+    if R <= 2048:
+        yr, accr = oracle.grouped_w8a8_f16(aq_r, as_r, w.numpy(), ws.numpy(), seg_r,
+                                           row_index=ri, want_acc=True)
+        assert np.array_equal(acc.cpu().numpy(), accr)
+        assert np.array_equal(y.cpu().numpy().view(np.uint16), yr.view(np.uint16))
+    else:  # sample rows: each sorted row r is expert e's GEMM of its own activation row
+        rng = np.random.default_rng(T)
+        rows = np.unique(np.concatenate([[0, R - 1], rng.choice(R, 64, replace=False)]))
+        expert = np.searchsorted(seg_r, rows, side="right") - 1
+        src = ri[rows] if ri is not None else rows
+        accs = np.stack([oracle.gemm_i8(aq_r[s_:s_ + 1], w.numpy()[e])[0]
+                         for s_, e in zip(src, expert)])
+        assert np.array_equal(acc.cpu().numpy()[rows], accs)
+        ys = np.stack([oracle.dequant_f16(a[None], as_r[s_:s_ + 1], ws.numpy()[e])[0]
+                       for a, s_, e in zip(accs, src, expert)])
+        assert np.array_equal(y.cpu().numpy()[rows].view(np.uint16), ys.view(np.uint16))
+
+
+@pytest.mark.parametrize("T", [16, 256])
+def test_combine_bitexact(pkg, wl, cuda, T):
+    E, k, H = wl.MOE["experts"], wl.MOE["top_k"], wl.MOE["hidden"]
+    topw, topi = _routing(wl, T, E, k, seed=T + 9)
+    _, _, pos = pkg.moe_sort(topi.cuda(), E)
+    y = wl.activations(T * k, H, seed=T + 10)
+    out = pkg.moe_combine(y.cuda(), topi.cuda(), topw.cuda(), pos)
+    _, _, _, pos_r = oracle.moe_sort(topi.numpy(), E)
+    out_r = oracle.moe_combine_f16(y.numpy(), topi.numpy(), topw.numpy(), pos_r)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), out_r.view(np.uint16))
+
+
+def _small_moe(pkg, wl, E=16, H=256, I=128, k=4, seed=0):
+    """Experts quantized from N(0, 0.05^2) fp16 weights, as the reference's MoE
+    tests build them (tests/test_deepseek.py:219-227)."""
+    g = torch.Generator().manual_seed(seed)
+    experts = []
+    for e in range(E):
+        gu = (torch.randn(2 * I, H, generator=g) * 0.05).half()
+        dn = (torch.randn(H, I, generator=g) * 0.05).half()
+        experts.append((pkg.to_qtensor(gu.cuda()), pkg.to_qtensor(dn.cuda())))
+    gate = (torch.randn(E, H, generator=g) * 0.05).half().cuda()
+    return pkg.SparseMoE(gate=gate, experts=experts, top_k=k, norm_topk_prob=True)
+
+
+@pytest.mark.parametrize("T", [1, 7, 64, 600])
+def test_sparse_moe_equals_expert_loop(pkg, wl, cuda, T):
+    """The grouped module output equals the reference's loop run over the same
+    W8A8 linears (`_experts_loop` drives ops.linear per expert), bit for bit."""
+    moe = _small_moe(pkg, wl)
+    x = (wl.activations(T, 256, seed=T) * 0.5).cuda().reshape(1, T, 256)
+    xf = x.reshape(-1, 256)
+    with torch.inference_mode():
+        topw, topi = moe.route(xf)
+        grouped = moe.experts_grouped(xf, topw, topi)
+        looped = moe._experts_loop(xf, topw, topi)
+        torch.cuda.synchronize()
+        assert torch.equal(grouped, looped)
+        y = moe(x)
+    assert y.shape == x.shape and torch.isfinite(y).all()
+
+
+def test_sparse_moe_close_to_cpu_reference(pkg, wl, cuda):
+    """Against the CPU restatement of the loop with oracle linears: the routed
+    int8 GEMMs match exactly; silu runs on different devices, so the end result is
+    compared with a tolerance."""
+    moe = _small_moe(pkg, wl, seed=3)
+    T = 40
+    x = (wl.activations(T, 256, seed=99) * 0.5)
+    xf = x.cuda()
+    with torch.inference_mode():
+        topw, topi = moe.route(xf)
+        out = moe.experts_grouped(xf, topw, topi).cpu().float().numpy()
+    ref = reference_moe_loop(x.numpy(), topi.cpu().numpy(), topw.cpu().numpy(),
+                             moe.w_gate_up.cpu().numpy(), moe.s_gate_up.cpu().numpy(),
+                             moe.w_down.cpu().numpy(), moe.s_down.cpu().numpy()).astype(np.float32)
+    cos = (out * ref).sum() / np.sqrt((out * out).sum() * (ref * ref).sum())
+    rel = np.linalg.norm(out - ref) / np.linalg.norm(ref)
+    print(f"grouped MoE vs CPU loop: cos {cos:.6f}, relative error {rel:.2e}", flush=True)
+    assert cos > 0.999 and rel < 2e-2
