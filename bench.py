@@ -1,0 +1,365 @@
+"""Benchmark of the W8A8 linear path on one MI355X.
+
+Headline (the `value`): Qwen3-8B decode linears -- fused QKV [6144, 4096],
+O [4096, 4096], gate_up [24576, 4096], down [4096, 12288] -- at
+M in {1, 4, 16, 64}, over a 36-layer pool of distinct int8 weights (6.95 GB,
+so every weight byte streams from HBM, not from the 256 MB Infinity Cache).
+One step = every (M, layer, linear) once: 576 linears, each a per-token
+quantize launch plus a GEMM launch, captured in one HIP graph and replayed.
+value = algorithmic bytes of the step / step time, in GB/s, where one linear
+moves N*K (W int8) + 4N (w_s) + 2MK (x fp16) + 2MN (y fp16) bytes.
+
+Also reported (same JSON line):
+  roofline      the M <= 16 decode GEMM kernel, timed per launch with HIP events
+                on the launch stream, against the 8 TB/s HBM peak
+  prefill       M in {512, 2048, 4096} on the four shapes: int8 TOPS against the
+                5.0 POPS dense int8 MFMA peak
+  moe           grouped expert GEMMs, 128 experts, top-8, T in {16, 256, 4096}
+  stack         36 layers x 4 linears at decode M=32 then prefill M=2048
+  cpu_baseline  the reference's CPU path for the same linears (dequantize the
+                weight on every call, then F.linear in fp16;
+                fni8serve/layers/linear.py:28-31, :70-71), on a bounded sample
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+import __graft_entry__  # noqa: E402
+
+METRIC = "int8 TOPS & HBM GB/s (% of roofline), Qwen3-8B W8A8 linears M=1..4096, 1 GPU"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def build_pool(wl, pkg, layers, device):
+    """36 layers x 4 linears of distinct random int8 weights, generated on the GPU."""
+    pool = []
+    for layer in range(layers):
+        entry = {}
+        for i, (name, (N, K)) in enumerate(wl.QWEN3_8B_LINEARS.items()):
+            q, s = wl.weight_i8(N, K, seed=1000 * layer + i, device=device)
+            entry[name] = pkg.QTensor(q, s, scheme="per_row_i8")
+        pool.append(entry)
+    return pool
+
+
+def decode_step_fn(pkg, pool, xs_by_m):
+    def step():
+        for M, xm in xs_by_m.items():
+            for layer in pool:
+                for name, qt in layer.items():
+                    pkg.linear(xm[qt.data.shape[1]], qt)
+    return step
+
+
+def decode_bytes(wl, layers, ms):
+    tot = 0
+    for M in ms:
+        for (N, K) in wl.QWEN3_8B_LINEARS.values():
+            tot += layers * wl.linear_bytes(M, N, K)
+    return tot
+
+
+def time_graph(step, warmup, steps):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(3):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return start.elapsed_time(end) / steps, wall, g
+
+
+def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
+    """Per-launch HIP-event timing of the decode GEMM kernel (pre-quantized
+    activations, so only the GEMM launch sits between the two events)."""
+    xq = {}
+    for M in ms:
+        for K in (4096, 12288):
+            x = wl.activations(M, K, seed=77 + M, device="cpu").to(device)
+            xq[(M, K)] = pkg.quantize_rowwise(x)
+    ev = []
+    meta = []
+    # Hold the stream with a GPU-side sleep while every launch is enqueued, so
+    # the events bracket back-to-back kernel execution, not host gaps.
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.0e8))
+    for _ in range(reps):
+        for M in ms:
+            for layer in pool:
+                for name, qt in layer.items():
+                    N, K = qt.data.shape
+                    a, s = xq[(M, K)]
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    pkg.gemm_w8a8(a, s, qt)
+                    e1.record()
+                    ev.append((e0, e1))
+                    meta.append((name, M, N, K))
+    torch.cuda.synchronize()
+    tot_b, tot_t = 0, 0.0
+    per = {}
+    for (e0, e1), (name, M, N, K) in zip(ev, meta):
+        t = e0.elapsed_time(e1) * 1e-3
+        b = wl.linear_bytes(M, N, K)
+        tot_b += b
+        tot_t += t
+        k = f"{name}_M{M}"
+        pb, pt, pn = per.get(k, (0, 0.0, 0))
+        per[k] = (pb + b, pt + t, pn + 1)
+    achieved = tot_b / tot_t / 1e9
+    n_launch = len(ev)
+    return {
+        "kernel": "gemm_skinny_kernel<MT=1,*,*,*,false> (decode GEMM, M<=16; the "
+                  "launch-weighted mean over its instantiations)",
+        "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+        "avg_launch_us": round(tot_t / n_launch * 1e6, 3),
+        "algorithmic_bytes_per_launch": int(tot_b / n_launch),
+        "launches": n_launch,
+        "per_shape_GBps": {k: round(b / t / 1e9, 1) for k, (b, t, n) in per.items()},
+        "per_shape_us": {k: round(t / n * 1e6, 2) for k, (b, t, n) in per.items()},
+    }
+
+
+def time_eager(fn, reps):
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def prefill_section(pkg, wl, pool, device, ms=(512, 2048, 4096)):
+    out = {}
+    layers = pool[:8]
+    for M in ms:
+        xs = {K: wl.activations(M, K, seed=300 + M, device="cpu").to(device) for K in (4096, 12288)}
+        for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
+            idx = [0]
+
+            def fn(name=name, K=K):
+                qt = layers[idx[0] % len(layers)][name]
+                idx[0] += 1
+                pkg.linear(xs[K], qt)
+            t = time_eager(fn, reps=8)
+            ops = wl.linear_ops(M, N, K)
+            b = wl.linear_bytes(M, N, K)
+            out[f"{name}_M{M}"] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 1),
+                                   "pct_mfma_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS * 100, 1),
+                                   "GBps": round(b / t / 1e9, 1)}
+        del xs
+    return out
+
+
+def moe_section(pkg, wl, device, ts=(16, 256, 4096)):
+    E, k, H, I = (wl.MOE[n] for n in ("experts", "top_k", "hidden", "inter"))
+    copies = []
+    for c in range(2):  # two copies of all experts (1.2 GB): rotate past the MALL
+        wg, sg = wl.expert_weights(E, 2 * I, H, seed=500 + c, device=device)
+        wd, sd = wl.expert_weights(E, H, I, seed=600 + c, device=device)
+        copies.append((wg, sg, wd, sd))
+    out = {}
+    for T in ts:
+        x = wl.activations(T, H, seed=T, device="cpu").to(device)
+        topw, topi = wl.route(wl.router_logits(T, E, seed=T + 1), k)
+        topw, topi = topw.to(device), topi.to(device)
+        active = int(torch.unique(topi).numel())
+        seg, rt, pos = pkg.moe_sort(topi, E)
+        xq, xs = pkg.quantize_rowwise(x)
+        R = T * k
+        h_act = (torch.randn(R, I, device=device) * 0.5).half()
+        aq, as_ = pkg.quantize_rowwise(h_act)
+        idx = [0]
+
+        def gate_up():
+            wg, sg, _, _ = copies[idx[0] % 2]
+            idx[0] += 1
+            pkg.gemm_w8a8_grouped(xq, xs, wg, sg, seg, R, row_index=rt)
+
+        def down():
+            _, _, wd, sd = copies[idx[0] % 2]
+            idx[0] += 1
+            pkg.gemm_w8a8_grouped(aq, as_, wd, sd, seg, R)
+        t_gu = time_eager(gate_up, reps=6)
+        t_dn = time_eager(down, reps=6)
+        b = wl.grouped_bytes(active, R, 2 * I, H) + wl.grouped_bytes(active, R, H, I)
+        ops = wl.linear_ops(R, 2 * I, H) + wl.linear_ops(R, H, I)
+        t = t_gu + t_dn
+        out[f"T{T}"] = {"active_experts": active, "rows": R, "gate_up_us": round(t_gu * 1e6, 2),
+                        "down_us": round(t_dn * 1e6, 2), "GBps": round(b / t / 1e9, 1),
+                        "pct_hbm_peak": round(b / t / 1e9 / HBM_PEAK_GBS * 100, 1),
+                        "TOPS": round(ops / t / 1e12, 2),
+                        "pct_mfma_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS * 100, 2)}
+    return out
+
+
+def stack_section(pkg, wl, pool, device):
+    out = {}
+    for M in (32, 2048):
+        xs = {K: wl.activations(M, K, seed=900 + M, device="cpu").to(device) for K in (4096, 12288)}
+
+        def fn():
+            for layer in pool:
+                for qt in layer.values():
+                    pkg.linear(xs[qt.data.shape[1]], qt)
+        t = time_eager(fn, reps=3)
+        b = sum(len(pool) * wl.linear_bytes(M, N, K) for N, K in wl.QWEN3_8B_LINEARS.values())
+        ops = sum(len(pool) * wl.linear_ops(M, N, K) for N, K in wl.QWEN3_8B_LINEARS.values())
+        out[f"M{M}"] = {"ms": round(t * 1e3, 3), "GBps": round(b / t / 1e9, 1),
+                        "TOPS": round(ops / t / 1e12, 1)}
+    return out
+
+
+def cpu_baseline(wl, budget_s=20.0):
+    """The reference's CPU linear (dequantize W per call, then F.linear in fp16),
+    on one layer's four linears at M in {1, 4, 16, 64}; time-bounded."""
+    from oracle.reference_cpu import reference_cpu_linear
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    tot_b, tot_t, done = 0, 0.0, []
+    t_start = time.perf_counter()
+    for M in (1, 4, 16, 64):
+        for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
+            if time.perf_counter() - t_start > budget_s:
+                break
+            q, s = wl.weight_i8(N, K, seed=11)
+            x = wl.activations(M, K, seed=12)
+            reference_cpu_linear(x, q, s)  # warm
+            runs = []
+            for _ in range(3):
+                t0 = time.perf_counter()
+                reference_cpu_linear(x, q, s)
+                runs.append(time.perf_counter() - t0)
+            dt = sorted(runs)[1]
+            tot_b += wl.linear_bytes(M, N, K)
+            tot_t += dt
+            done.append(f"{name}@M{M}")
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"reference CPU path (fp16 dequant of W per call + F.linear), one layer: "
+                      f"{len(done)} linears ({', '.join(done)}), median of 3 timed calls each "
+                      f"after a warm call, sum of medians {tot_t:.1f} s, cpu '{model}', "
+                      f"os.cpu_count={os.cpu_count()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=36)
+    ap.add_argument("--sections", default="roofline,prefill,moe,stack,cpu")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path "
+              "is single-GPU; multi-GPU sharding is a design note only)", file=sys.stderr)
+        sys.exit(2)
+    sections = set(s for s in args.sections.split(",") if s)
+
+    pkg = __graft_entry__.load_package()
+    from importlib import import_module
+    wl = import_module("fni8serve_amd.workloads")
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+
+    log(f"building {args.layers}-layer weight pool on {torch.cuda.get_device_name(device)}")
+    pool = build_pool(wl, pkg, args.layers, device)
+    pool_gb = sum(qt.data.numel() + qt.scale.numel() * 4 for layer in pool for qt in layer.values()) / 1e9
+    xs_by_m = {M: {K: wl.activations(M, K, seed=M * 10 + K, device="cpu").to(device)
+                   for K in (4096, 12288)} for M in wl.DECODE_M}
+
+    step = decode_step_fn(pkg, pool, xs_by_m)
+    ms_per_step, wall, graph = time_graph(step, args.warmup, args.steps)
+    step_bytes = decode_bytes(wl, len(pool), wl.DECODE_M)
+    step_ops = sum(len(pool) * wl.linear_ops(M, N, K) for M in wl.DECODE_M
+                   for N, K in wl.QWEN3_8B_LINEARS.values())
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"decode step: {ms_per_step:.3f} ms, {value:.1f} GB/s ({value / HBM_PEAK_GBS * 100:.1f}% of "
+        f"8 TB/s), wall {wall:.2f} s for {args.steps} steps")
+    del graph
+
+    per_m = {}
+    for M in wl.DECODE_M:
+        sub = decode_step_fn(pkg, pool, {M: xs_by_m[M]})
+        t, _, g = time_graph(sub, 1, 5)
+        b = decode_bytes(wl, len(pool), (M,))
+        per_m[f"M{M}"] = {"ms": round(t, 3), "GBps": round(b / (t * 1e-3) / 1e9, 1),
+                          "pct_hbm_peak": round(b / (t * 1e-3) / 1e9 / HBM_PEAK_GBS * 100, 1)}
+        del g
+    log(f"decode per M: {per_m}")
+
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "Qwen3-8B decode W8A8 linears (fused QKV 6144x4096, O 4096x4096, "
+                               "gate_up 24576x4096, down 4096x12288) x 36 layers of distinct "
+                               "weights, M in {1,4,16,64}, per-token quant + int8 GEMM + fp16 "
+                               "epilogue per linear, one HIP graph per step",
+                   "linears_per_step": 4 * len(pool) * len(wl.DECODE_M),
+                   "weight_pool_GB": round(pool_gb, 2), "step_bytes": step_bytes,
+                   "step_int8_ops": step_ops, "x": "fp16 N(0,1), 1% outliers x20",
+                   "pct_hbm_peak": round(value / HBM_PEAK_GBS * 100, 2),
+                   "decode_TOPS": round(step_ops / (ms_per_step * 1e-3) / 1e12, 2),
+                   "per_M": per_m},
+    }
+    if "roofline" in sections:
+        result["roofline"] = kernel_roofline(pkg, wl, pool, device)
+        log(f"roofline: {result['roofline']}")
+    if "prefill" in sections:
+        result["prefill"] = prefill_section(pkg, wl, pool, device)
+        log(f"prefill: {result['prefill']}")
+    if "moe" in sections:
+        result["moe"] = moe_section(pkg, wl, device)
+        log(f"moe: {result['moe']}")
+    if "stack" in sections:
+        result["stack"] = stack_section(pkg, wl, pool, device)
+        log(f"stack: {result['stack']}")
+    if "cpu" in sections:
+        result["cpu_baseline"] = cpu_baseline(wl)
+        log(f"cpu_baseline: {result['cpu_baseline']}")
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

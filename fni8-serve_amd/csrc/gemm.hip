@@ -33,10 +33,21 @@ __device__ __forceinline__ i32x4 ld16(const int8_t* p) {
     return *reinterpret_cast<const i32x4*>(p);
 }
 
+// Streaming load: non-temporal hint, for data read exactly once.
+__device__ __forceinline__ i32x4 ld16_stream(const int8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
+}
+
 // ---------------------------------------------------------------------------
 // skinny kernel
 // ---------------------------------------------------------------------------
-template <int MT, int WAVES, int U, bool GROUPED>
+// MT: 16-row blocks of activations (M <= 16 * MT); NB: 16-row blocks of weight
+// rows per workgroup (every wave streams all NB blocks over its K share, so
+// each activation fragment feeds NB MFMAs); WAVES: waves splitting K;
+// U: 64-byte K units per loop trip (U * NB 16-byte weight loads in flight per
+// lane).  Weight loads are non-temporal: each byte is used once, so they are
+// kept from displacing the activations in L2.
+template <int MT, int NB, int WAVES, int U, bool GROUPED>
 __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(
     const int8_t* __restrict__ aq, int64_t lda, const float* __restrict__ as,
     const int32_t* __restrict__ row_index, int M, int K, const int8_t* __restrict__ w,
@@ -44,7 +55,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy,
     int32_t* __restrict__ acc_out) {
     constexpr int BM = 16 * MT;
-    __shared__ i32x4 red[WAVES][MT][64];
+    constexpr int BN = 16 * NB;
+    __shared__ i32x4 red[WAVES][MT * NB][64];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -67,14 +79,21 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(
     }
 
     const int r = lane & 15, g = lane >> 4;
-    const int n = nt * 16 + r;
-    const bool nvalid = n < N;
-    const int8_t* wrow = wexp + (int64_t)(nvalid ? n : 0) * K + g * 16;
+    const int8_t* wrow[NB];
+    bool nvalid[NB];
+    float wsc[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int n = nt * BN + b * 16 + r;
+        nvalid[b] = n < N;
+        wrow[b] = wexp + (int64_t)(nvalid[b] ? n : 0) * K + g * 16;
+        wsc[b] = nvalid[b] ? wsexp[n] : 0.f;  // epilogue scale, fetched early
+    }
     const int8_t* arow[MT];
     bool avalid[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-        int mr = m0 + mt * 16 + r;
+        const int mr = m0 + mt * 16 + r;
         avalid[mt] = mr < m1;
         int src = mr;
         if (GROUPED && row_index != nullptr && avalid[mt]) src = row_index[mr];
@@ -86,17 +105,22 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(
     const int u0 = wave * per;
     const int u1 = min(units, u0 + per);
 
-    i32x4 acc[MT];
+    i32x4 acc[MT][NB];
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) acc[mt] = i32x4{0, 0, 0, 0};
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[mt][b] = i32x4{0, 0, 0, 0};
 
     for (int u = u0; u < u1; u += U) {
-        i32x4 bw[U];
+        i32x4 bw[NB][U];
         i32x4 ax[MT][U];
 #pragma unroll
         for (int j = 0; j < U; j++) {
             const bool ok = (u + j) < u1;
-            bw[j] = (ok && nvalid) ? ld16(wrow + (int64_t)(u + j) * 64) : i32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+                bw[b][j] = (ok && nvalid[b]) ? ld16_stream(wrow[b] + (int64_t)(u + j) * 64)
+                                             : i32x4{0, 0, 0, 0};
 #pragma unroll
             for (int mt = 0; mt < MT; mt++)
                 ax[mt][j] = (ok && avalid[mt]) ? ld16(arow[mt] + (int64_t)(u + j) * 64)
@@ -105,28 +129,37 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(
 #pragma unroll
         for (int j = 0; j < U; j++)
 #pragma unroll
-            for (int mt = 0; mt < MT; mt++) acc[mt] = mfma_i8(ax[mt][j], bw[j], acc[mt]);
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++) acc[mt][b] = mfma_i8(ax[mt][j], bw[b][j], acc[mt][b]);
     }
 
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++) red[wave][mt][lane] = acc[mt];
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) red[wave][mt * NB + b][lane] = acc[mt][b];
     __syncthreads();
 
-    for (int idx = threadIdx.x; idx < MT * 64; idx += WAVES * 64) {
-        const int mt = idx >> 6, ln = idx & 63;
-        i32x4 s = red[0][mt][ln];
+    // Each (m-block, n-block) result is summed over the waves by one wave-sized
+    // group of threads; a thread keeps the lane layout of the MFMA result.
+    for (int idx = threadIdx.x; idx < MT * NB * 64; idx += WAVES * 64) {
+        const int mb = idx >> 6, ln = idx & 63;
+        const int mt = mb / NB, b = mb % NB;
+        i32x4 s = red[0][mb][ln];
 #pragma unroll
-        for (int wv = 1; wv < WAVES; wv++) s += red[wv][mt][ln];
-        const int col = nt * 16 + (ln & 15);
+        for (int wv = 1; wv < WAVES; wv++) s += red[wv][mb][ln];
+        const int col = nt * BN + b * 16 + (ln & 15);
         if (col >= N) continue;
-        const float wsc = wsexp[col];
+        // ln == lane (the stride is a whole number of waves), so wsc[b] is this
+        // column's scale.
+        const float wscale = wsc[b];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int mr = m0 + mt * 16 + (ln >> 4) * 4 + i;
             if (mr >= m1) continue;
             int src = mr;
             if (GROUPED && row_index != nullptr) src = row_index[mr];
-            y[(int64_t)mr * ldy + col] = fni8::dequant_one(s[i], as[src], wsc, bexp, col);
+            y[(int64_t)mr * ldy + col] = fni8::dequant_one(s[i], as[src], wscale, bexp, col);
             if (acc_out) acc_out[(int64_t)mr * N + col] = s[i];
         }
     }
@@ -340,13 +373,13 @@ struct Args {
     int32_t* acc_out;
 };
 
-template <int MT, int WAVES, bool GROUPED>
+template <int MT, int NB, int WAVES, int U, bool GROUPED>
 void launch_skinny(const Args& a, unsigned mslots, hipStream_t st) {
-    const unsigned ntn = (unsigned)((a.N + 15) / 16);
+    const unsigned ntn = (unsigned)((a.N + 16 * NB - 1) / (16 * NB));
     dim3 grid = GROUPED ? dim3(mslots, ntn) : dim3(ntn, mslots), block(WAVES * 64);
-    hipLaunchKernelGGL((gemm_skinny_kernel<MT, WAVES, 4, GROUPED>), grid, block, 0, st, a.aq,
-                       a.lda, a.as, a.row_index, a.M, a.K, a.w, a.ws, a.N, a.E, a.seg_off,
-                       a.bias, a.y, a.ldy, a.acc_out);
+    hipLaunchKernelGGL((gemm_skinny_kernel<MT, NB, WAVES, U, GROUPED>), grid, block, 0, st,
+                       a.aq, a.lda, a.as, a.row_index, a.M, a.K, a.w, a.ws, a.N, a.E,
+                       a.seg_off, a.bias, a.y, a.ldy, a.acc_out);
 }
 
 template <int BM, int BN, int WM, int WN, bool GROUPED>
@@ -384,15 +417,31 @@ void launch_generic(const Args& a, hipStream_t st) {
                        a.ldy, a.acc_out);
 }
 
-template <int MT, bool GROUPED>
-void skinny_by_waves(const Args& a, unsigned ytiles, hipStream_t st) {
-    const int units = a.K / 64;
-    if (units >= 64)
-        launch_skinny<MT, 16, GROUPED>(a, ytiles, st);
-    else if (units >= 16)
-        launch_skinny<MT, 8, GROUPED>(a, ytiles, st);
-    else
-        launch_skinny<MT, 4, GROUPED>(a, ytiles, st);
+// Decode launch shapes, chosen by measurement on MI355X (weights streamed from
+// HBM): 4-wave groups with 16 loads in flight per lane for K = 4096, 8 waves x 4
+// loads for long K; two weight blocks per wave once M >= 16 on wide N so each
+// activation fragment is reused.
+void launch_decode(const Args& a, hipStream_t st) {
+    const int M = a.M, N = a.N, K = a.K;
+    const bool wide = N >= 16384, longk = K >= 8192, mid = N >= 6144;
+    if (M <= 4) {
+        if (longk) launch_skinny<1, 1, 8, 4, false>(a, 1, st);
+        else launch_skinny<1, 1, 4, 16, false>(a, 1, st);
+    } else if (M <= 16) {
+        if (wide) launch_skinny<1, 2, 2, 16, false>(a, 1, st);
+        else if (longk) launch_skinny<1, 1, 16, 4, false>(a, 1, st);
+        else if (mid) launch_skinny<1, 2, 2, 16, false>(a, 1, st);
+        else launch_skinny<1, 1, 4, 16, false>(a, 1, st);
+    } else if (M <= 32) {
+        if (wide || (mid && !longk)) launch_skinny<2, 2, 4, 8, false>(a, 1, st);
+        else if (longk) launch_skinny<2, 1, 16, 4, false>(a, 1, st);
+        else launch_skinny<2, 1, 4, 16, false>(a, 1, st);
+    } else {
+        if (wide) launch_skinny<4, 2, 4, 4, false>(a, 1, st);
+        else if (longk) launch_skinny<4, 1, 8, 4, false>(a, 1, st);
+        else if (mid) launch_skinny<4, 2, 8, 2, false>(a, 1, st);
+        else launch_skinny<4, 1, 4, 8, false>(a, 1, st);
+    }
 }
 
 }  // namespace
@@ -417,16 +466,14 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
         const double avg = (double)M / (double)E;
         if (avg <= 48.0) {
             const unsigned slots = (unsigned)((M + 15) / 16 + E);
-            skinny_by_waves<1, true>(a, slots, st);
+            if (K >= 1024) launch_skinny<1, 1, 4, 8, true>(a, slots, st);
+            else launch_skinny<1, 1, 2, 8, true>(a, slots, st);
         } else {
             const unsigned slots = (unsigned)((M + 127) / 128 + E);
             rc = launch_tile<128, 128, 2, 2, true>(a, slots, st);
         }
     } else if (M <= 64) {
-        const unsigned ytiles = 1;
-        if (M <= 16) skinny_by_waves<1, false>(a, ytiles, st);
-        else if (M <= 32) skinny_by_waves<2, false>(a, ytiles, st);
-        else skinny_by_waves<4, false>(a, ytiles, st);
+        launch_decode(a, st);
     } else {
         const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
         if (t256 >= 256)
