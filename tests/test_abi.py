@@ -1,0 +1,72 @@
+"""The C-ABI library loads without a GPU, exports every entry point declared in
+include/fni8amd.h, and rejects bad arguments before touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "fni8amd.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(fni8_\w+)\s*\(", text, re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib(pkg):
+    from importlib import import_module
+    return import_module("fni8serve_amd._lib").load()
+
+
+def test_header_declares_the_entry_points():
+    names = _declared()
+    for n in ("fni8_quantize_rowwise_f16", "fni8_gemm_w8a8", "fni8_linear_w8a8_f16",
+              "fni8_moe_sort", "fni8_gemm_w8a8_grouped", "fni8_moe_combine_f16",
+              "fni8_strerror", "fni8_last_error", "fni8_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), f"{name} declared in fni8amd.h but not exported"
+
+
+def test_binding_covers_every_declared_compute_entry(pkg):
+    from importlib import import_module
+    sigs = import_module("fni8serve_amd._lib").SIGNATURES
+    strings = import_module("fni8serve_amd._lib").STRING_FUNCS
+    assert set(_declared()) == set(sigs) | set(strings)
+
+
+def test_version_and_error_strings(lib):
+    assert lib.fni8_version().decode().startswith("fni8amd")
+    assert lib.fni8_strerror(0) == b"ok"
+    assert b"NULL" in lib.fni8_strerror(-1)
+    assert lib.fni8_strerror(-99) == b"unknown error"
+
+
+def test_argument_errors_return_before_any_launch(lib):
+    P = ctypes.c_void_p
+    fake = P(0x1000)  # never dereferenced: every call below fails its argument checks
+    # NULL required pointer
+    rc = lib.fni8_linear_w8a8_f16(None, 64, 1, 64, fake, fake, 8, None, fake, 8, fake, fake, None, None)
+    assert rc == -1 and b"required" in lib.fni8_last_error()
+    # K not a multiple of 4 (the reference's quantizable rule, convert.py:128)
+    rc = lib.fni8_linear_w8a8_f16(fake, 66, 1, 66, fake, fake, 8, None, fake, 8, fake, fake, None, None)
+    assert rc == -2 and b"multiple of 4" in lib.fni8_last_error()
+    # leading dimension shorter than the row
+    rc = lib.fni8_linear_w8a8_f16(fake, 32, 1, 64, fake, fake, 8, None, fake, 8, fake, fake, None, None)
+    assert rc == -4
+    # misaligned int8 operand
+    rc = lib.fni8_gemm_w8a8(P(0x1001), 64, fake, 1, 64, fake, fake, 8, None, fake, 8, None, None)
+    assert rc == -3
+    # grouped: bad expert count; sort: top-k beyond the combine limit
+    rc = lib.fni8_gemm_w8a8_grouped(fake, fake, None, 8, 64, fake, fake, 0, 8, fake, None, fake, None, None)
+    assert rc == -2
+    rc = lib.fni8_moe_sort(fake, 4, 33, 8, fake, fake, fake, None)
+    assert rc == -2
+    rc = lib.fni8_quantize_rowwise_f16(fake, -1, 64, 64, fake, 64, fake, None)
+    assert rc == -2
