@@ -469,17 +469,25 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
             if (K >= 1024) launch_skinny<1, 1, 4, 8, true>(a, slots, st);
             else launch_skinny<1, 1, 2, 8, true>(a, slots, st);
         } else {
-            const unsigned slots = (unsigned)((M + 127) / 128 + E);
-            rc = launch_tile<128, 128, 2, 2, true>(a, slots, st);
+            rc = launch_tile32(aq, lda, as, row_index, M, K, w, ws, N, E, seg_off, bias, y, ldy,
+                               acc_out, st);
+            if (rc == 1) {
+                const unsigned slots = (unsigned)((M + 127) / 128 + E);
+                rc = launch_tile<128, 128, 2, 2, true>(a, slots, st);
+            }
         }
     } else if (M <= 64) {
         launch_decode(a, st);
     } else {
-        const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-        if (t256 >= 256)
-            rc = launch_tile<256, 256, 2, 4, false>(a, 0, st);
-        else
-            rc = launch_tile<128, 128, 2, 2, false>(a, 0, st);
+        rc = launch_tile32(aq, lda, as, row_index, M, K, w, ws, N, 0, seg_off, bias, y, ldy,
+                           acc_out, st);
+        if (rc == 1) {  // K not a multiple of 128: the 16x16x64 tile kernel
+            const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+            if (t256 >= 256)
+                rc = launch_tile<256, 256, 2, 4, false>(a, 0, st);
+            else
+                rc = launch_tile<128, 128, 2, 2, false>(a, 0, st);
+        }
     }
     if (rc) return rc;
     hipError_t e = hipGetLastError();

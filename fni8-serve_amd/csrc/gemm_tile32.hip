@@ -1,0 +1,316 @@
+// Prefill GEMM on v_mfma_i32_32x32x32_i8 (gfx950).
+//
+// On gfx950 the 32x32x32 int8 MFMA retires twice the int8 work per cycle of
+// the 16x16x64 form (measured on MI355X: 4.76 vs 2.64 POPS of pure MFMA), so
+// the compute-bound path uses it exclusively.
+//
+// Workgroup: 8 waves (2 x 4), macro tile BM x BN, each wave a (BM/2) x (BN/4)
+// block of 32x32 accumulators (16 int32 per lane each).  K is consumed in BK-byte
+// steps through two LDS stages (rows padded by 16 bytes: conflict-free 16-byte
+// reads for the 32-row MFMA fragment pattern), with global loads staged in
+// registers two steps ahead: step k+2 is fetched while step k computes.  The
+// steady-state loop is branch-free (two steps per trip, tail peeled), which
+// keeps every register-array index static.
+//
+// Epilogue: the accumulators go to LDS as int32 (half the tile at a time),
+// then every thread streams 16-byte rows back, applies
+// fp16(((float)acc * as[m]) * ws[n] (+ bias[n])) with a wave-uniform row scale
+// and writes 8 contiguous bytes per lane -- coalesced output with almost no
+// live registers.
+#include <type_traits>
+
+#include "common.h"
+
+namespace {
+
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ i32x4 ld16(const int8_t* p) {
+    return *reinterpret_cast<const i32x4*>(p);
+}
+
+template <int BM, int BN, int BK, bool GROUPED, bool WRITE_ACC>
+__global__ __launch_bounds__(512) void gemm_tile32_kernel(
+    const int8_t* __restrict__ aq, int64_t lda, const float* __restrict__ as,
+    const int32_t* __restrict__ row_index, int M, int K, const int8_t* __restrict__ w,
+    const float* __restrict__ ws, int N, int E, const int32_t* __restrict__ seg_off,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy,
+    int32_t* __restrict__ acc_out) {
+    constexpr int WAVES_M = 2, WAVES_N = 4, NT = 512;
+    constexpr int LDSR = BK + 16;   // padded LDS row (bytes)
+    constexpr int CPR = BK / 16;    // 16-byte chunks per row per step
+    constexpr int WTM = BM / WAVES_M, WTN = BN / WAVES_N;
+    constexpr int FM = WTM / 32, FN = WTN / 32;
+    constexpr int A_CH = BM * CPR / NT, B_CH = BN * CPR / NT;
+    static_assert(A_CH * NT == BM * CPR && B_CH * NT == BN * CPR, "tile/threads mismatch");
+    constexpr int BUF = (BM + BN) * LDSR;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int ntiles_n = (N + BN - 1) / BN;
+
+    int m0, m1, n0;
+    const int8_t* wexp = w;
+    const float* wsexp = ws;
+    const uint16_t* bexp = bias;
+    if constexpr (GROUPED) {  // x = segment tile slot, y = n-tile
+        n0 = blockIdx.y * BN;
+        int e;
+        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, e, m0, m1)) return;
+        wexp += (int64_t)e * N * K;
+        wsexp += (int64_t)e * N;
+        if (bias) bexp += (int64_t)e * N;
+    } else {
+        // XCD-aware order: consecutive ids land on different XCDs, so give each
+        // XCD a contiguous band of tiles, walked 8 m-tiles at a time.
+        const int ntiles_m = (M + BM - 1) / BM;
+        const int total = ntiles_m * ntiles_n;
+        int bid = blockIdx.x;
+        if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+        constexpr int GM = 8;
+        const int group = bid / (GM * ntiles_n);
+        const int first_m = group * GM;
+        const int gsize = min(ntiles_m - first_m, GM);
+        const int in_group = bid - group * GM * ntiles_n;
+        m0 = (first_m + in_group % gsize) * BM;
+        m1 = min(M, m0 + BM);
+        n0 = (in_group / gsize) * BN;
+    }
+
+    // Global sources of this thread's chunks; rows past the end are clamped to
+    // the last valid row (their products land in rows that are never written).
+    const int8_t* asrc[A_CH];
+    const int8_t* bsrc[B_CH];
+#pragma unroll
+    for (int i = 0; i < A_CH; i++) {
+        const int c = tid + i * NT;
+        int mr = m0 + c / CPR;
+        mr = mr < m1 ? mr : m1 - 1;
+        int src = mr;
+        if (GROUPED && row_index != nullptr) src = row_index[mr];
+        asrc[i] = aq + (int64_t)src * lda + (c % CPR) * 16;
+    }
+#pragma unroll
+    for (int i = 0; i < B_CH; i++) {
+        const int c = tid + i * NT;
+        int nr = n0 + c / CPR;
+        nr = nr < N ? nr : N - 1;
+        bsrc[i] = wexp + (int64_t)nr * K + (c % CPR) * 16;
+    }
+
+    i32x4 ra[2][A_CH], rb[2][B_CH];
+    auto gload = [&](int kt, auto slot_c) {
+        constexpr int slot = decltype(slot_c)::value;
+        const int64_t ko = (int64_t)kt * BK;
+#pragma unroll
+        for (int i = 0; i < A_CH; i++) ra[slot][i] = ld16(asrc[i] + ko);
+#pragma unroll
+        for (int i = 0; i < B_CH; i++) rb[slot][i] = ld16(bsrc[i] + ko);
+    };
+    auto sstore = [&](auto buf_c, auto slot_c) {
+        constexpr int buf = decltype(buf_c)::value, slot = decltype(slot_c)::value;
+        int8_t* base = smem + buf * BUF;
+#pragma unroll
+        for (int i = 0; i < A_CH; i++) {
+            const int c = tid + i * NT;
+            *reinterpret_cast<i32x4*>(base + (c / CPR) * LDSR + (c % CPR) * 16) = ra[slot][i];
+        }
+#pragma unroll
+        for (int i = 0; i < B_CH; i++) {
+            const int c = tid + i * NT;
+            *reinterpret_cast<i32x4*>(base + (BM + c / CPR) * LDSR + (c % CPR) * 16) = rb[slot][i];
+        }
+    };
+
+    i32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = i32x16{};
+
+    // Fragment read: lane l takes row l%32 of a 32-row block and the k-half
+    // (l/32)*16 of each 32-byte k sub-step -- the 32x32x32 operand layout.
+    const int fo = (lane & 31) * LDSR + (lane >> 5) * 16;
+    auto compute = [&](auto buf_c) {
+        constexpr int buf = decltype(buf_c)::value;
+        const int8_t* ab = smem + buf * BUF + (wm * WTM) * LDSR + fo;
+        const int8_t* bb = smem + buf * BUF + (BM + wn * WTN) * LDSR + fo;
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ks++) {
+            i32x4 af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+                af[i] = *reinterpret_cast<const i32x4*>(ab + i * 32 * LDSR + ks * 32);
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+                bf[j] = *reinterpret_cast<const i32x4*>(bb + j * 32 * LDSR + ks * 32);
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    const int KT = K / BK;  // even and >= 2 (checked by the launcher)
+    gload(0, C0{});
+    gload(1, C1{});
+    sstore(C0{}, C0{});
+    __syncthreads();
+    for (int kt = 0; kt < KT - 2; kt += 2) {
+        gload(kt + 2, C0{});
+        compute(C0{});
+        sstore(C1{}, C1{});
+        __syncthreads();
+        gload(kt + 3, C1{});
+        compute(C1{});
+        sstore(C0{}, C0{});
+        __syncthreads();
+    }
+    compute(C0{});
+    sstore(C1{}, C1{});
+    __syncthreads();
+    compute(C1{});
+    __syncthreads();  // every wave is done with the LDS stages
+
+    // ---- epilogue -----------------------------------------------------------
+    constexpr int HALF = BM / 2;          // rows staged per pass (one wave-row)
+    constexpr int OTS = BN + 8;           // int32 row stride of the staging tile
+    float* as_l = reinterpret_cast<float*>(smem);
+    float* ws_l = as_l + BM;
+    int32_t* ot = reinterpret_cast<int32_t*>(ws_l + BN);
+    for (int t = tid; t < BM; t += NT) {
+        const int mr = m0 + t;
+        float v = 0.f;
+        if (mr < m1) v = as[(GROUPED && row_index != nullptr) ? row_index[mr] : mr];
+        as_l[t] = v;
+    }
+    for (int t = tid; t < BN; t += NT) ws_l[t] = (n0 + t < N) ? wsexp[n0 + t] : 0.f;
+
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+        if (wm == pass) {
+            // lane l, register r of block (i, j): row 8*(r/4) + 4*(l/32) + r%4, col l%32
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        const int col = wn * WTN + j * 32 + (lane & 31);
+                        ot[row * OTS + col] = acc[i][j][r];
+                    }
+        }
+        __syncthreads();
+        // stream the staged half: BN/4 chunks of 4 columns per row; a wave covers
+        // whole rows, so the row scale is uniform across the wave
+        constexpr int CHR = BN / 4;
+        for (int c = tid; c < HALF * CHR; c += NT) {
+            const int rl = c / CHR, cl = (c % CHR) * 4;
+            const int row_t = pass * HALF + rl;
+            const int mr = m0 + row_t;
+            const int col = n0 + cl;
+            if (mr >= m1 || col >= N) continue;
+            const i32x4 a4 = *reinterpret_cast<const i32x4*>(ot + rl * OTS + cl);
+            const float asc = as_l[row_t];
+            uint16_t h[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float v = (float)a4[q] * asc;
+                v = v * ws_l[cl + q];
+                if (bexp != nullptr && col + q < N) v = v + fni8::h2f(bexp[col + q]);
+                h[q] = fni8::f2h(v);
+            }
+            uint16_t* yp = y + (int64_t)mr * ldy + col;
+            if (col + 3 < N && ((uintptr_t)yp & 7) == 0) {
+                uint2 pk;
+                pk.x = h[0] | ((uint32_t)h[1] << 16);
+                pk.y = h[2] | ((uint32_t)h[3] << 16);
+                *reinterpret_cast<uint2*>(yp) = pk;
+            } else {
+                for (int q = 0; q < 4 && col + q < N; q++) yp[q] = h[q];
+            }
+            if constexpr (WRITE_ACC) {
+                for (int q = 0; q < 4 && col + q < N; q++) acc_out[(int64_t)mr * N + col + q] = a4[q];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <int BM, int BN, int BK, bool GROUPED>
+int launch(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index, int M,
+           int K, const int8_t* w, const float* ws, int N, int E, const int32_t* seg_off,
+           const uint16_t* bias, uint16_t* y, int64_t ldy, int32_t* acc_out, unsigned slots,
+           hipStream_t st) {
+    constexpr size_t main_lds = 2 * (BM + BN) * (BK + 16);
+    constexpr size_t epi_lds = (BM + BN) * 4 + (BM / 2) * (BN + 8) * 4;
+    constexpr size_t lds = main_lds > epi_lds ? main_lds : epi_lds;
+    static_assert(lds <= 160 * 1024, "LDS budget");
+    const unsigned ntn = (unsigned)((N + BN - 1) / BN);
+    dim3 grid = GROUPED ? dim3(slots, ntn) : dim3(ntn * (unsigned)((M + BM - 1) / BM));
+    auto run = [&](auto kern) -> int {
+        // The LDS limit is a per-function attribute; setting it again with the
+        // same value is idempotent, so a race between threads is harmless.
+        static bool attr_set = false;
+        if (!attr_set) {
+            hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+            if (e != hipSuccess) {
+                fni8h::set_error_detail("LDS attribute (%zu bytes): %s", lds, hipGetErrorString(e));
+                return FNI8_ERR_LAUNCH;
+            }
+            attr_set = true;
+        }
+        hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, aq, lda, as, row_index, M, K, w, ws, N,
+                           E, seg_off, bias, y, ldy, acc_out);
+        return FNI8_OK;
+    };
+    if (acc_out) return run(gemm_tile32_kernel<BM, BN, BK, GROUPED, true>);
+    return run(gemm_tile32_kernel<BM, BN, BK, GROUPED, false>);
+}
+
+}  // namespace
+
+namespace fni8h {
+
+// Returns 1 if the shape was not taken (the caller falls back), else an FNI8 code.
+int launch_tile32(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index,
+                  int64_t M, int64_t K, const int8_t* w, const float* ws, int64_t N, int64_t E,
+                  const int32_t* seg_off, const uint16_t* bias, uint16_t* y, int64_t ldy,
+                  int32_t* acc_out, hipStream_t st) {
+    // K steps of 128 (or 64) bytes, an even number of them
+    const bool k128 = K % 256 == 0, k64 = !k128 && K % 128 == 0;
+    if (!(k128 || k64)) return 1;
+    const int m = (int)M, k = (int)K, n = (int)N, e = (int)E;
+    if (E > 0) {
+        const unsigned slots = (unsigned)((M + 127) / 128 + E);
+        if (k128)
+            return launch<128, 256, 128, true>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
+                                               bias, y, ldy, acc_out, slots, st);
+        return launch<128, 256, 64, true>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off, bias,
+                                          y, ldy, acc_out, slots, st);
+    }
+    // Dense: the biggest tile that still fills the 256 CUs in whole rounds.
+    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+    const double fill256 = (double)t256 / (double)(((t256 + 255) / 256) * 256);
+    if (t256 >= 256 && fill256 >= 0.7) {
+        if (k128)
+            return launch<256, 256, 128, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
+                                                bias, y, ldy, acc_out, 0, st);
+        return launch<256, 256, 64, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
+                                           bias, y, ldy, acc_out, 0, st);
+    }
+    if (k128)
+        return launch<128, 256, 128, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
+                                            bias, y, ldy, acc_out, 0, st);
+    return launch<128, 256, 64, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off, bias, y,
+                                       ldy, acc_out, 0, st);
+}
+
+}  // namespace fni8h
