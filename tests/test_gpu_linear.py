@@ -59,7 +59,7 @@ def _check_full(pkg, x, q, s, bias=None, tag=""):
           f"max rel err {rel:.3g}", flush=True)
 
 
-@pytest.mark.parametrize("M", [1, 4, 16, 64])
+@pytest.mark.parametrize("M", [1, 4, 16, 32, 64])
 @pytest.mark.parametrize("name", ["qkv", "o", "gate_up", "down"])
 def test_decode_linear_bitexact(pkg, wl, cuda, name, M):
     N, K = wl.QWEN3_8B_LINEARS[name]
@@ -77,7 +77,7 @@ def test_cpu_case_bitexact(pkg, wl, cuda):
 
 @pytest.mark.parametrize("M,N,K", [
     (3, 100, 256), (17, 48, 512), (33, 4096, 4096), (65, 256, 1024), (100, 640, 2048),
-    (257, 384, 1024), (130, 130, 128),
+    (257, 384, 1024), (130, 130, 128), (8, 16, 64), (64, 1000, 192),
     (5, 64, 1028), (7, 33, 36), (70, 20, 100),     # K % 64 != 0: generic kernel
 ])
 def test_ragged_shapes_bitexact(pkg, wl, cuda, M, N, K):
