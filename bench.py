@@ -98,44 +98,49 @@ def time_graph(step, warmup, steps):
 
 
 def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
-    """Per-launch HIP-event timing of the decode GEMM kernel (pre-quantized
-    activations, so only the GEMM launch sits between the two events)."""
+    """HIP-event timing of the decode GEMM kernel: for each (linear, M), one
+    burst of its 36 per-layer launches (pre-quantized activations, so only GEMM
+    launches run) between two events on the launch stream.  Every burst is
+    enqueued behind a GPU-side sleep, so the events bracket back-to-back kernel
+    execution with no host gaps; the per-launch mean of such bursts agrees with
+    rocprofv3's kernel durations."""
     xq = {}
     for M in ms:
         for K in (4096, 12288):
             x = wl.activations(M, K, seed=77 + M, device="cpu").to(device)
             xq[(M, K)] = pkg.quantize_rowwise(x)
-    ev = []
-    meta = []
-    # Hold the stream with a GPU-side sleep while every launch is enqueued, so
-    # the events bracket back-to-back kernel execution, not host gaps.
+    names = list(wl.QWEN3_8B_LINEARS)
+    for M in ms:  # warm every launch shape once
+        for name in names:
+            a, s = xq[(M, pool[0][name].data.shape[1])]
+            pkg.gemm_w8a8(a, s, pool[0][name])
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2.0e8))
+    bursts = []
     for _ in range(reps):
         for M in ms:
-            for layer in pool:
-                for name, qt in layer.items():
-                    N, K = qt.data.shape
-                    a, s = xq[(M, K)]
-                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                    e0.record()
-                    pkg.gemm_w8a8(a, s, qt)
-                    e1.record()
-                    ev.append((e0, e1))
-                    meta.append((name, M, N, K))
+            for name in names:
+                N, K = wl.QWEN3_8B_LINEARS[name]
+                a, s = xq[(M, K)]
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for layer in pool:
+                    pkg.gemm_w8a8(a, s, layer[name])
+                e1.record()
+                bursts.append((e0, e1, name, M, N, K, len(pool)))
     torch.cuda.synchronize()
-    tot_b, tot_t = 0, 0.0
+    tot_b, tot_t, n_launch = 0, 0.0, 0
     per = {}
-    for (e0, e1), (name, M, N, K) in zip(ev, meta):
+    for e0, e1, name, M, N, K, n in bursts:
         t = e0.elapsed_time(e1) * 1e-3
-        b = wl.linear_bytes(M, N, K)
+        b = wl.linear_bytes(M, N, K) * n
         tot_b += b
         tot_t += t
+        n_launch += n
         k = f"{name}_M{M}"
         pb, pt, pn = per.get(k, (0, 0.0, 0))
-        per[k] = (pb + b, pt + t, pn + 1)
+        per[k] = (pb + b, pt + t, pn + n)
     achieved = tot_b / tot_t / 1e9
-    n_launch = len(ev)
     return {
         "kernel": "gemm_skinny_kernel<MT=1,*,*,*,false> (decode GEMM, M<=16; the "
                   "launch-weighted mean over its instantiations)",
@@ -147,6 +152,29 @@ def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
         "per_shape_GBps": {k: round(b / t / 1e9, 1) for k, (b, t, n) in per.items()},
         "per_shape_us": {k: round(t / n * 1e6, 2) for k, (b, t, n) in per.items()},
     }
+
+
+def copy_calibration(device, mb=512):
+    """A plain device copy of known size, for scaling the FETCH_SIZE / WRITE_SIZE
+    counters of a profiled run (the copy moves exactly `mb` MiB each way)."""
+    src = torch.empty(mb << 20, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    src.fill_(1)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"bytes_each_way": mb << 20, "launches": 3}
+
+
+def load_traffic(root):
+    """Per-launch HBM bytes of the decode GEMM measured by rocprofv3 counters,
+    kept as a text summary under profiles/ (null when absent)."""
+    path = os.path.join(root, "profiles", "decode_gemm_hbm_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def time_eager(fn, reps):
@@ -345,7 +373,13 @@ def main():
     }
     if "roofline" in sections:
         result["roofline"] = kernel_roofline(pkg, wl, pool, device)
+        tr = load_traffic(ROOT)
+        if tr is not None:
+            result["roofline"]["traffic"] = tr["hbm_bytes_per_launch"]
+            result["roofline"]["traffic_source"] = tr["source"]
         log(f"roofline: {result['roofline']}")
+    if "copycal" in sections:
+        result["copy_calibration"] = copy_calibration(device)
     if "prefill" in sections:
         result["prefill"] = prefill_section(pkg, wl, pool, device)
         log(f"prefill: {result['prefill']}")
