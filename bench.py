@@ -98,22 +98,21 @@ def time_graph(step, warmup, steps):
 
 
 def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
-    """HIP-event timing of the decode GEMM kernel: for each (linear, M), one
-    burst of its 36 per-layer launches (pre-quantized activations, so only GEMM
-    launches run) between two events on the launch stream.  Every burst is
+    """HIP-event timing of the decode linear (M <= 16): for each (linear, M), one
+    burst of its 36 per-layer calls between two events on the launch stream.
+    For M <= 4 a call is one launch (the fused quantize + GEMV kernel); for
+    M = 16 it is the quantize launch plus the GEMM launch.  Every burst is
     enqueued behind a GPU-side sleep, so the events bracket back-to-back kernel
-    execution with no host gaps; the per-launch mean of such bursts agrees with
+    execution with no host gaps; the per-call mean of such bursts agrees with
     rocprofv3's kernel durations."""
-    xq = {}
+    xs = {}
     for M in ms:
         for K in (4096, 12288):
-            x = wl.activations(M, K, seed=77 + M, device="cpu").to(device)
-            xq[(M, K)] = pkg.quantize_rowwise(x)
+            xs[(M, K)] = wl.activations(M, K, seed=77 + M, device="cpu").to(device)
     names = list(wl.QWEN3_8B_LINEARS)
     for M in ms:  # warm every launch shape once
         for name in names:
-            a, s = xq[(M, pool[0][name].data.shape[1])]
-            pkg.gemm_w8a8(a, s, pool[0][name])
+            pkg.linear(xs[(M, pool[0][name].data.shape[1])], pool[0][name])
     torch.cuda.synchronize()
     torch.cuda._sleep(int(2.0e8))
     bursts = []
@@ -121,11 +120,11 @@ def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
         for M in ms:
             for name in names:
                 N, K = wl.QWEN3_8B_LINEARS[name]
-                a, s = xq[(M, K)]
+                x = xs[(M, K)]
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record()
                 for layer in pool:
-                    pkg.gemm_w8a8(a, s, layer[name])
+                    pkg.linear(x, layer[name])
                 e1.record()
                 bursts.append((e0, e1, name, M, N, K, len(pool)))
     torch.cuda.synchronize()
@@ -141,14 +140,20 @@ def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
         pb, pt, pn = per.get(k, (0, 0.0, 0))
         per[k] = (pb + b, pt + t, pn + n)
     achieved = tot_b / tot_t / 1e9
+    by_m = {}
+    for k, (b, t, n) in per.items():
+        m = k.rsplit("_M", 1)[1]
+        bb, tt = by_m.get(m, (0, 0.0))
+        by_m[m] = (bb + b, tt + t)
     return {
-        "kernel": "gemm_skinny_kernel<MT=1,*,*,*,false> (decode GEMM, M<=16; the "
-                  "launch-weighted mean over its instantiations)",
+        "kernel": "decode W8A8 linear, M <= 16: decode_gemv_kernel (quantization fused, one "
+                  "launch) for M <= 4; quant_rowwise_regs_kernel + gemm_skinny_kernel for M = 16",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "avg_launch_us": round(tot_t / n_launch * 1e6, 3),
         "algorithmic_bytes_per_launch": int(tot_b / n_launch),
         "launches": n_launch,
+        "frac_by_M": {f"M{m}": round(b / t / 1e9 / HBM_PEAK_GBS, 4) for m, (b, t) in by_m.items()},
         "per_shape_GBps": {k: round(b / t / 1e9, 1) for k, (b, t, n) in per.items()},
         "per_shape_us": {k: round(t / n * 1e6, 2) for k, (b, t, n) in per.items()},
     }

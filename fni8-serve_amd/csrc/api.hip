@@ -145,6 +145,10 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
     rc = check_device();
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
+    // Decode sizes: one launch, the quantization fused into the GEMV.
+    rc = fni8h::launch_decode_fused((const uint16_t*)x, ldx, M, K, w, ws, N, (const uint16_t*)bias,
+                                    (uint16_t*)y, ldy, xq, xs, acc_out, st);
+    if (rc != 1) return rc;
     rc = fni8h::launch_quant_rowwise((const uint16_t*)x, M, K, ldx, xq, K, xs, st);
     if (rc) return rc;
     return fni8h::launch_gemm(xq, K, xs, nullptr, M, K, w, ws, N, 0, nullptr,

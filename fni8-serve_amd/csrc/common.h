@@ -131,6 +131,15 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
                 int64_t M, int64_t K, const int8_t* w, const float* ws, int64_t N,
                 int64_t E, const int32_t* seg_off, const uint16_t* bias, uint16_t* y,
                 int64_t ldy, int32_t* acc_out, hipStream_t st);
+// Decode (M <= 4) GEMV with the quantization fused in; returns 1 when the
+// shape is not taken (the caller then quantizes and runs launch_gemm).
+int launch_decode_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                        const float* ws, int64_t N, const uint16_t* bias, uint16_t* y, int64_t ldy,
+                        int8_t* xq_out, float* xs_out, int32_t* acc_out, hipStream_t st);
+// The same GEMV on pre-quantized activations; returns 1 when not taken.
+int launch_decode_q(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                    const int8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
+                    int64_t ldy, int32_t* acc_out, hipStream_t st);
 int launch_tile32(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index,
                   int64_t M, int64_t K, const int8_t* w, const float* ws, int64_t N, int64_t E,
                   const int32_t* seg_off, const uint16_t* bias, uint16_t* y, int64_t ldy,

@@ -477,7 +477,11 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
             }
         }
     } else if (M <= 64) {
-        launch_decode(a, st);
+        rc = launch_decode_q(aq, lda, as, M, K, w, ws, N, bias, y, ldy, acc_out, st);
+        if (rc == 1) {
+            rc = FNI8_OK;
+            launch_decode(a, st);
+        }
     } else {
         rc = launch_tile32(aq, lda, as, row_index, M, K, w, ws, N, 0, seg_off, bias, y, ldy,
                            acc_out, st);

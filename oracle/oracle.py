@@ -18,6 +18,9 @@ parity pinning (how each function is checked, in tests/test_oracle.py):
       indexing fails the check.
   moe_sort / grouped_w8a8_f16 / moe_combine_f16 -- brute force against the
       reference's per-expert loop restated with `nonzero` in numpy (moe.py:218-224).
+  quant_identity_check -- not an oracle function: the exhaustive proof, over
+      every fp16 (x, amax) pair, that the division-free quantization of the GPU
+      decode kernel reproduces quant_rowwise_f16's division (quant_identity.c).
 """
 from __future__ import annotations
 
@@ -56,9 +59,11 @@ def _load():
     lib.oracle_moe_sort.argtypes = [P, I, I, I, P, P, P, P]
     lib.oracle_grouped_w8a8_f16.argtypes = [P, P, I, P, P, P, I, I, P, P, P, P]
     lib.oracle_moe_combine_f16.argtypes = [P, I, P, P, P, I, I, P]
+    lib.oracle_quant_identity_check.argtypes = [ctypes.c_int, P]
     for fn in ("oracle_f16_to_f32_n", "oracle_f32_to_f16_n", "oracle_quant_rowwise_f16",
                "oracle_gemm_i8", "oracle_dequant_f16", "oracle_linear_w8a8_f16",
-               "oracle_grouped_w8a8_f16", "oracle_moe_combine_f16"):
+               "oracle_grouped_w8a8_f16", "oracle_moe_combine_f16",
+               "oracle_quant_identity_check"):
         getattr(lib, fn).restype = None
     _lib = lib
     return lib
@@ -179,3 +184,13 @@ def moe_combine_f16(y_sorted, topi, topw, pos):
     out = np.empty((T, H), np.float16)
     _load().oracle_moe_combine_f16(_p(y_sorted), H, _p(topi), _p(topw), _p(pos), T, k, _p(out))
     return out
+
+
+def quant_identity_check(corrected: bool = True):
+    """(pairs, quotient mismatches for x != 0, rounded mismatches) of the
+    division-free quantization against fl(x / s) over every fp16 (x, amax) pair
+    with |x| <= amax (quant_identity.c); corrected=False drops the FMA
+    correction step."""
+    out = np.zeros(3, np.int64)
+    _load().oracle_quant_identity_check(0 if corrected else 1, _p(out))
+    return tuple(int(v) for v in out)

@@ -146,6 +146,24 @@ def test_quant_matches_numpy_fp32_restatement():
     assert np.array_equal(s, s_np.astype(np.float32)) and np.array_equal(q, q_np)
 
 
+def test_division_free_quant_identity_exhaustive():
+    """The GPU decode kernel quantizes with y = fl(1/s), t = fl(x*y),
+    v = fma(fma(-t, s, x), y, t) instead of fl(x/s).  Over every fp16 amax and
+    every fp16 x with |x| <= amax (about 10^9 pairs) the quotient is the same
+    bits for x != 0 and the rounded integer is always the same."""
+    pairs, bad_quot, bad_int = oracle.quant_identity_check()
+    assert pairs == 1007713280
+    assert bad_quot == 0 and bad_int == 0
+
+
+def test_division_free_quant_identity_check_detects_a_missing_correction():
+    """Negative control: without the FMA correction (q = rint(fl(x * fl(1/s))))
+    the same exhaustive sweep finds quotient and rounded-integer mismatches."""
+    pairs, bad_quot, bad_int = oracle.quant_identity_check(corrected=False)
+    assert pairs == 1007713280
+    assert bad_quot > 0 and bad_int > 0
+
+
 # ---- int8 GEMM -------------------------------------------------------------
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 4096), (8, 300, 1024), (33, 17, 12288), (5, 7, 4)])
