@@ -147,7 +147,7 @@ def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
         by_m[m] = (bb + b, tt + t)
     return {
         "kernel": "decode W8A8 linear, M <= 16: decode_gemv_kernel (quantization fused, one "
-                  "launch) for M <= 4; quant_rowwise_regs_kernel + gemm_skinny_kernel for M = 16",
+                  "launch) for M <= 4; quant_rowwise_regs_kernel + decode_mfma_kernel for M = 16",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "avg_launch_us": round(tot_t / n_launch * 1e6, 3),

@@ -60,6 +60,71 @@ __device__ __forceinline__ uint16_t dequant_one(int32_t acc, float as, float ws,
     return f2h(v);
 }
 
+// ---- wave reductions and the division-free quantization --------------------
+// DPP lane permutations (gfx9 encodings).
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i within 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15-i within 16
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
+}
+
+// Sum over each group of 8 consecutive lanes; every lane of the group gets it.
+__device__ __forceinline__ int sum8(int v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    return v;
+}
+
+// Max over the wave of non-negative values, returned as a wave-uniform value.
+__device__ __forceinline__ uint32_t wave_max_uniform(uint32_t v) {
+    int t = (int)v;
+    int o;
+    o = dpp<kDppXor1>(t); t = o > t ? o : t;
+    o = dpp<kDppXor2>(t); t = o > t ? o : t;
+    o = dpp<kDppHalfMirror>(t); t = o > t ? o : t;
+    o = dpp<kDppMirror>(t); t = o > t ? o : t;
+    int a = __builtin_amdgcn_readlane(t, 0), b = __builtin_amdgcn_readlane(t, 16);
+    int c = __builtin_amdgcn_readlane(t, 32), d = __builtin_amdgcn_readlane(t, 48);
+    a = a > b ? a : b;
+    c = c > d ? c : d;
+    return (uint32_t)(a > c ? a : c);
+}
+
+// q for one fp16 value given the row's finite scale s and yr = fl(1/s)
+// (correctly rounded): t = fl(x*yr), r = fma(-t, s, x) is exact, and
+// fma(r, yr, t) == fl(x/s) for every non-zero fp16 |x| <= amax (Markstein's
+// correction; checked exhaustively over all fp16 (x, amax) pairs by the CPU
+// test suite), so rint of it equals quant_one's rint(x / s).
+__device__ __forceinline__ uint32_t quant_fast(float x, float s, float yr) {
+    const float t = x * yr;
+    const float r = __builtin_fmaf(-t, s, x);
+    float v = __builtin_fmaf(r, yr, t);
+    v = __builtin_rintf(v);
+    v = __builtin_fminf(__builtin_fmaxf(v, -FNI8_QMAX), FNI8_QMAX);
+    return (uint32_t)(int32_t)v & 0xffu;
+}
+
+// 8 fp16 (one 16-byte chunk) -> 8 int8; zeros unless `live` (finite scale, real row).
+__device__ __forceinline__ uint2 quant_chunk(uint4 v, float s, float yr, bool live) {
+    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+    uint32_t out[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const uint32_t a = w4[2 * i], b = w4[2 * i + 1];
+        const uint32_t q0 = quant_fast(h2f((uint16_t)(a & 0xffffu)), s, yr);
+        const uint32_t q1 = quant_fast(h2f((uint16_t)(a >> 16)), s, yr);
+        const uint32_t q2 = quant_fast(h2f((uint16_t)(b & 0xffffu)), s, yr);
+        const uint32_t q3 = quant_fast(h2f((uint16_t)(b >> 16)), s, yr);
+        out[i] = live ? (q0 | (q1 << 8) | (q2 << 16) | (q3 << 24)) : 0u;
+    }
+    return make_uint2(out[0], out[1]);
+}
+
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -140,6 +205,10 @@ int launch_decode_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, co
 int launch_decode_q(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
                     const int8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
                     int64_t ldy, int32_t* acc_out, hipStream_t st);
+// Decode GEMM (M <= 64, pre-quantized activations) on MFMA; returns 1 when not taken.
+int launch_decode_mfma(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                       const int8_t* w, const float* ws, int64_t N, const uint16_t* bias,
+                       uint16_t* y, int64_t ldy, int32_t* acc_out, hipStream_t st);
 int launch_tile32(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index,
                   int64_t M, int64_t K, const int8_t* w, const float* ws, int64_t N, int64_t E,
                   const int32_t* seg_off, const uint16_t* bias, uint16_t* y, int64_t ldy,

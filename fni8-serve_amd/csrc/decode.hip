@@ -37,66 +37,6 @@ __device__ __forceinline__ i32x4 ld16_nt(const int8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
 }
 
-// DPP lane permutations (gfx9 encodings).
-constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
-constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
-constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7-i within 8
-constexpr int kDppMirror = 0x140;      // lane i <-> 15-i within 16
-
-template <int CTRL>
-__device__ __forceinline__ int dpp(int v) {
-    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xf, 0xf, false);
-}
-
-// Sum over each group of 8 consecutive lanes; every lane of the group gets it.
-__device__ __forceinline__ int sum8(int v) {
-    v += dpp<kDppXor1>(v);
-    v += dpp<kDppXor2>(v);
-    v += dpp<kDppHalfMirror>(v);
-    return v;
-}
-
-// Max over the wave of non-negative values, returned as a wave-uniform value.
-__device__ __forceinline__ uint32_t wave_max_uniform(uint32_t v) {
-    int t = (int)v;
-    int o;
-    o = dpp<kDppXor1>(t); t = o > t ? o : t;
-    o = dpp<kDppXor2>(t); t = o > t ? o : t;
-    o = dpp<kDppHalfMirror>(t); t = o > t ? o : t;
-    o = dpp<kDppMirror>(t); t = o > t ? o : t;
-    int a = __builtin_amdgcn_readlane(t, 0), b = __builtin_amdgcn_readlane(t, 16);
-    int c = __builtin_amdgcn_readlane(t, 32), d = __builtin_amdgcn_readlane(t, 48);
-    a = a > b ? a : b;
-    c = c > d ? c : d;
-    return (uint32_t)(a > c ? a : c);
-}
-
-// q for one fp16 value given the row's finite scale s and yr = fl(1/s).
-__device__ __forceinline__ uint32_t quant_fast(float x, float s, float yr) {
-    const float t = x * yr;
-    const float r = __builtin_fmaf(-t, s, x);
-    float v = __builtin_fmaf(r, yr, t);
-    v = __builtin_rintf(v);
-    v = __builtin_fminf(__builtin_fmaxf(v, -FNI8_QMAX), FNI8_QMAX);
-    return (uint32_t)(int32_t)v & 0xffu;
-}
-
-// 8 fp16 (one 16-byte chunk) -> 8 int8; zeros unless `live` (finite scale, real row).
-__device__ __forceinline__ uint2 quant_chunk(uint4 v, float s, float yr, bool live) {
-    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-    uint32_t out[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint32_t a = w4[2 * i], b = w4[2 * i + 1];
-        const uint32_t q0 = quant_fast(fni8::h2f((uint16_t)(a & 0xffffu)), s, yr);
-        const uint32_t q1 = quant_fast(fni8::h2f((uint16_t)(a >> 16)), s, yr);
-        const uint32_t q2 = quant_fast(fni8::h2f((uint16_t)(b & 0xffffu)), s, yr);
-        const uint32_t q3 = quant_fast(fni8::h2f((uint16_t)(b >> 16)), s, yr);
-        out[i] = live ? (q0 | (q1 << 8) | (q2 << 16) | (q3 << 24)) : 0u;
-    }
-    return make_uint2(out[0], out[1]);
-}
-
 // MM: token rows handled (M <= MM); RH: 8-row groups per workgroup; WAVES: K
 // split; SB: 128-byte slabs per load batch (must divide each wave's share);
 // KCH: 16-byte chunks of each activation row per thread (K <= 16 * KCH * 64 *
@@ -178,7 +118,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
                     am = hi > am ? hi : am;
                 }
             }
-            am = wave_max_uniform(am);
+            am = fni8::wave_max_uniform(am);
             if (lane == 0) amx[wave * MM + m] = am;
         }
         __syncthreads();
@@ -198,7 +138,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
             for (int i = 0; i < KCH; i++) {
                 const int ch = tid + i * NT;
                 if (ch < chunks) {
-                    const uint2 q = quant_chunk(xr[m][i], s, yr, live);
+                    const uint2 q = fni8::quant_chunk(xr[m][i], s, yr, live);
                     *reinterpret_cast<uint2*>(xq_l + (size_t)m * K + ch * 8) = q;
                     if (xq_out != nullptr && blockIdx.x == 0 && m < M)
                         *reinterpret_cast<uint2*>(xq_out + (int64_t)m * K + ch * 8) = q;
@@ -276,7 +216,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
     for (int h = 0; h < RH; h++)
 #pragma unroll
         for (int m = 0; m < MM; m++) {
-            const int a = sum8(acc[h][m]);
+            const int a = fni8::sum8(acc[h][m]);
             if (c == 0) red[(wave * MM + m) * ROWS + h * 8 + rq] = a;
         }
     __syncthreads();

@@ -478,6 +478,7 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
         }
     } else if (M <= 64) {
         rc = launch_decode_q(aq, lda, as, M, K, w, ws, N, bias, y, ldy, acc_out, st);
+        if (rc == 1) rc = launch_decode_mfma(aq, lda, as, M, K, w, ws, N, bias, y, ldy, acc_out, st);
         if (rc == 1) {
             rc = FNI8_OK;
             launch_decode(a, st);

@@ -1,8 +1,10 @@
 // Per-token symmetric int8 quantization of fp16 activations (gfx950).
 //
 // One workgroup per row.  The row's max magnitude is an integer max over the
-// fp16 magnitude bits (wave64 xor-shuffle reduction, then one LDS step across
-// waves); then q = clamp(rint(x / s), -127, 127) from the same registers.
+// fp16 magnitude bits (DPP reduction within the wave, then one LDS step across
+// waves); then q = clamp(rint(x / s), -127, 127) from the same registers,
+// computed without a per-element division (fni8::quant_chunk: one correctly
+// rounded reciprocal per row and an exact FMA correction).
 // HBM-bound: 2K bytes read + K + 4 written per row.
 #include "common.h"
 
@@ -37,29 +39,22 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rowwise_regs_kernel(
             amax = hi > amax ? hi : amax;
         }
     }
-    amax = fni8::wave_max_u32(amax);
+    amax = fni8::wave_max_uniform(amax);
     if ((tid & 63) == 0) red[tid >> 6] = amax;
     __syncthreads();
     amax = red[0];
 #pragma unroll
     for (int i = 1; i < kQuantThreads / 64; i++) amax = red[i] > amax ? red[i] : amax;
     const float sc = fni8::row_scale_from_bits(amax);
+    const bool live = __builtin_isfinite(sc);  // NaN/inf scale: every q is 0
+    const float yr = 1.0f / sc;                // correctly rounded (build flag)
     if (tid == 0) s[m] = sc;
 
 #pragma unroll
     for (int c = 0; c < CH; c++) {
         const int k = (c * kQuantThreads + tid) * 8;
         if (k >= K) continue;
-        const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-        uint32_t packed[2] = {0, 0};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int32_t q0 = fni8::quant_one(fni8::h2f((uint16_t)(w4[i] & 0xffffu)), sc);
-            const int32_t q1 = fni8::quant_one(fni8::h2f((uint16_t)(w4[i] >> 16)), sc);
-            const uint32_t pair = ((uint32_t)q0 & 0xffu) | (((uint32_t)q1 & 0xffu) << 8);
-            packed[i >> 1] |= pair << ((i & 1) * 16);
-        }
-        *reinterpret_cast<uint2*>(qr + k) = make_uint2(packed[0], packed[1]);
+        *reinterpret_cast<uint2*>(qr + k) = fni8::quant_chunk(v[c], sc, yr, live);
     }
 }
 

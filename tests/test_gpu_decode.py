@@ -1,6 +1,6 @@
-"""GPU parity of the decode path (M <= 4): the single-launch linear with the
-per-token quantization fused into the GEMV, and the same GEMV on pre-quantized
-activations.
+"""GPU parity of the decode path: for M <= 4 the single-launch linear with the
+per-token quantization fused into the GEMV (and the same GEMV on pre-quantized
+activations); for 4 < M <= 64 the quantize launch plus the MFMA decode GEMM.
 
 Bar: int8 activations, fp32 scales, int32 accumulators and fp16 outputs are
 bit-identical to the CPU oracle on the same seeded inputs.  The fused kernel
@@ -171,3 +171,36 @@ def test_fused_graph_replay(pkg, wl, cuda):
         eager = pkg.linear(xi, qt)
         torch.cuda.synchronize()
         assert torch.equal(static_y, eager)
+
+
+# ---- 4 < M <= 64: quantize launch + MFMA decode GEMM -------------------------
+
+@pytest.mark.parametrize("M", [5, 17, 33, 63])
+@pytest.mark.parametrize("name", ["qkv", "o", "gate_up", "down"])
+def test_mfma_decode_bitexact(pkg, wl, cuda, name, M):
+    N, K = wl.QWEN3_8B_LINEARS[name]
+    x = wl.activations(M, K, seed=600 + M)
+    q, s = wl.weight_i8(N, K, seed=SEEDS[name] + 40)
+    _linear_full(pkg, x, q, s, tag=f"mfma decode {name} M={M}")
+
+
+@pytest.mark.parametrize("M,N,K", [
+    (12, 48, 384),     # 3 slabs: one wave
+    (20, 100, 256),    # 2 slabs: two waves; N not a multiple of 16
+    (40, 70, 640),     # 5 slabs
+    (64, 16, 1024),
+    (9, 4096, 12288),
+])
+def test_mfma_decode_ragged_bitexact(pkg, wl, cuda, M, N, K):
+    x = wl.activations(M, K, seed=M * 3 + K)
+    q, s = wl.weight_i8(N, K, seed=N * 7 + K)
+    _linear_full(pkg, x, q, s, tag=f"mfma ragged M={M} N={N} K={K}")
+
+
+def test_mfma_decode_bias_and_stride(pkg, wl, cuda):
+    M, N, K = 20, 640, 2048
+    big = wl.activations(M, 2 * K, seed=91)
+    x = big[:, K:]
+    q, s = wl.weight_i8(N, K, seed=92)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(93)) * 2).half()
+    _linear_full(pkg, x, q, s, bias=bias, tag="mfma bias+stride M=20")
