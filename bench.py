@@ -4,14 +4,15 @@ Headline (the `value`): Qwen3-8B decode linears -- fused QKV [6144, 4096],
 O [4096, 4096], gate_up [24576, 4096], down [4096, 12288] -- at
 M in {1, 4, 16, 64}, over a 36-layer pool of distinct int8 weights (6.95 GB,
 so every weight byte streams from HBM, not from the 256 MB Infinity Cache).
-One step = every (M, layer, linear) once: 576 linears, each a per-token
-quantize launch plus a GEMM launch, captured in one HIP graph and replayed.
+One step = every (M, layer, linear) once: 576 linears, captured in one HIP
+graph and replayed.  A linear is one launch for M <= 4 (per-token quantization
+fused into the decode GEMV) and a quantize launch plus a GEMM launch above.
 value = algorithmic bytes of the step / step time, in GB/s, where one linear
 moves N*K (W int8) + 4N (w_s) + 2MK (x fp16) + 2MN (y fp16) bytes.
 
 Also reported (same JSON line):
-  roofline      the M <= 16 decode GEMM kernel, timed per launch with HIP events
-                on the launch stream, against the 8 TB/s HBM peak
+  roofline      the M <= 16 decode linear (its kernels), timed per call with HIP
+                events on the launch stream, against the 8 TB/s HBM peak
   prefill       M in {512, 2048, 4096} on the four shapes: int8 TOPS against the
                 5.0 POPS dense int8 MFMA peak
   moe           grouped expert GEMMs, 128 experts, top-8, T in {16, 256, 4096}
@@ -172,9 +173,9 @@ def copy_calibration(device, mb=512):
 
 
 def load_traffic(root):
-    """Per-launch HBM bytes of the decode GEMM measured by rocprofv3 counters,
+    """Per-call HBM bytes of the decode linear measured by rocprofv3 counters,
     kept as a text summary under profiles/ (null when absent)."""
-    path = os.path.join(root, "profiles", "decode_gemm_hbm_traffic.json")
+    path = os.path.join(root, "profiles", "decode_linear_hbm_traffic.json")
     try:
         with open(path) as f:
             return json.load(f)
@@ -275,9 +276,11 @@ def stack_section(pkg, wl, pool, device):
     return out
 
 
-def cpu_baseline(wl, budget_s=20.0):
+def cpu_baseline(wl, budget_s=40.0, per_linear_s=0.8):
     """The reference's CPU linear (dequantize W per call, then F.linear in fp16),
-    on one layer's four linears at M in {1, 4, 16, 64}; time-bounded."""
+    on one layer's four linears at M in {1, 4, 16, 64}: each linear is called
+    repeatedly for about `per_linear_s` seconds after a warm call (about 13 s of
+    CPU work in all), and the mean time per call is used."""
     from oracle.reference_cpu import reference_cpu_linear
 
     threads = len(os.sched_getaffinity(0))
@@ -291,12 +294,14 @@ def cpu_baseline(wl, budget_s=20.0):
             q, s = wl.weight_i8(N, K, seed=11)
             x = wl.activations(M, K, seed=12)
             reference_cpu_linear(x, q, s)  # warm
-            runs = []
-            for _ in range(3):
-                t0 = time.perf_counter()
+            calls, t0 = 0, time.perf_counter()
+            while True:
                 reference_cpu_linear(x, q, s)
-                runs.append(time.perf_counter() - t0)
-            dt = sorted(runs)[1]
+                calls += 1
+                el = time.perf_counter() - t0
+                if calls >= 3 and el >= per_linear_s:
+                    break
+            dt = el / calls
             tot_b += wl.linear_bytes(M, N, K)
             tot_t += dt
             done.append(f"{name}@M{M}")
@@ -309,9 +314,9 @@ def cpu_baseline(wl, budget_s=20.0):
     return {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"reference CPU path (fp16 dequant of W per call + F.linear), one layer: "
-                      f"{len(done)} linears ({', '.join(done)}), median of 3 timed calls each "
-                      f"after a warm call, sum of medians {tot_t:.1f} s, cpu '{model}', "
-                      f"os.cpu_count={os.cpu_count()}"}
+                      f"{len(done)} linears ({', '.join(done)}), each called repeatedly for "
+                      f"~{per_linear_s} s after a warm call (mean per call), {tot_t:.3f} s of "
+                      f"per-call time summed, cpu '{model}', os.cpu_count={os.cpu_count()}"}
 
 
 def main():
@@ -321,6 +326,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=36)
     ap.add_argument("--sections", default="roofline,prefill,moe,stack,cpu")
+    ap.add_argument("--no-step", action="store_true",
+                    help="skip the graph-replayed decode step (for counter runs of one section)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the path "
@@ -340,6 +347,12 @@ def main():
     xs_by_m = {M: {K: wl.activations(M, K, seed=M * 10 + K, device="cpu").to(device)
                    for K in (4096, 12288)} for M in wl.DECODE_M}
 
+    if args.no_step:
+        result = {"metric": METRIC, "value": None, "unit": "GB/s", "n_gpus": 1,
+                  "note": "decode step skipped (--no-step)"}
+        run_sections(result, sections, pkg, wl, pool, device)
+        print(json.dumps(result), flush=True)
+        return
     step = decode_step_fn(pkg, pool, xs_by_m)
     ms_per_step, wall, graph = time_graph(step, args.warmup, args.steps)
     step_bytes = decode_bytes(wl, len(pool), wl.DECODE_M)
@@ -376,6 +389,11 @@ def main():
                    "decode_TOPS": round(step_ops / (ms_per_step * 1e-3) / 1e12, 2),
                    "per_M": per_m},
     }
+    run_sections(result, sections, pkg, wl, pool, device)
+    print(json.dumps(result), flush=True)
+
+
+def run_sections(result, sections, pkg, wl, pool, device):
     if "roofline" in sections:
         result["roofline"] = kernel_roofline(pkg, wl, pool, device)
         tr = load_traffic(ROOT)
@@ -397,7 +415,6 @@ def main():
     if "cpu" in sections:
         result["cpu_baseline"] = cpu_baseline(wl)
         log(f"cpu_baseline: {result['cpu_baseline']}")
-    print(json.dumps(result), flush=True)
 
 
 if __name__ == "__main__":

@@ -28,8 +28,13 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// fp32 -> fp16, round to nearest even.  Emitted as its own v_cvt_f16_f32 so the
+// compiler cannot fold a preceding multiply into a mixed-precision FMA (whose
+// +0 addend would turn a -0 product into +0).
 __device__ __forceinline__ uint16_t f2h(float f) {
-    return __builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, round to nearest even
+    uint32_t r;
+    asm("v_cvt_f16_f32 %0, %1" : "=v"(r) : "v"(f));
+    return (uint16_t)(r & 0xffffu);
 }
 
 // Row scale from the max fp16 magnitude bits of the row.  Integer max over
