@@ -101,8 +101,9 @@ def time_graph(step, warmup, steps):
 def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
     """HIP-event timing of the decode linear (M <= 16): for each (linear, M), one
     burst of its 36 per-layer calls between two events on the launch stream.
-    For M <= 4 a call is one launch (the fused quantize + GEMV kernel); for
-    M = 16 it is the quantize launch plus the GEMM launch.  Every burst is
+    For M <= 4 a call is one launch (quantization fused: the dot4 GEMV at M = 1,
+    the MFMA kernel at M = 4); for M = 16 it is the quantize launch plus the
+    MFMA GEMM launch.  Every burst is
     enqueued behind a GPU-side sleep, so the events bracket back-to-back kernel
     execution with no host gaps; the per-call mean of such bursts agrees with
     rocprofv3's kernel durations."""
@@ -147,8 +148,9 @@ def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
         bb, tt = by_m.get(m, (0, 0.0))
         by_m[m] = (bb + b, tt + t)
     return {
-        "kernel": "decode W8A8 linear, M <= 16: decode_gemv_kernel (quantization fused, one "
-                  "launch) for M <= 4; quant_rowwise_regs_kernel + decode_mfma_kernel for M = 16",
+        "kernel": "decode W8A8 linear, M <= 16: one launch with the quantization fused for "
+                  "M <= 4 (decode_gemv_kernel at M = 1, decode_mfma_fused_kernel at M = 4); "
+                  "quant_rowwise_regs_kernel + decode_mfma_kernel for M = 16",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "avg_launch_us": round(tot_t / n_launch * 1e6, 3),

@@ -145,7 +145,15 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
     rc = check_device();
     if (rc) return rc;
     hipStream_t st = (hipStream_t)stream;
-    // Decode sizes: one launch, the quantization fused into the GEMV.
+    // Decode sizes: one launch, the quantization fused into the GEMM -- on MFMA
+    // for 3..4 tokens, as a dot4 GEMV for 1..2 (and shapes the MFMA kernel does
+    // not take), where the streaming loop without an LDS pass is faster.
+    if (M >= 3) {
+        rc = fni8h::launch_decode_mfma_fused((const uint16_t*)x, ldx, M, K, w, ws, N,
+                                             (const uint16_t*)bias, (uint16_t*)y, ldy, xq, xs,
+                                             acc_out, st);
+        if (rc != 1) return rc;
+    }
     rc = fni8h::launch_decode_fused((const uint16_t*)x, ldx, M, K, w, ws, N, (const uint16_t*)bias,
                                     (uint16_t*)y, ldy, xq, xs, acc_out, st);
     if (rc != 1) return rc;

@@ -210,6 +210,13 @@ int launch_decode_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, co
 int launch_decode_q(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
                     const int8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
                     int64_t ldy, int32_t* acc_out, hipStream_t st);
+// Decode GEMM on MFMA, fp16 activations quantized in the kernel (M <= 4, one
+// launch); xq_out (row stride K) and xs_out receive the quantized activations.
+// Returns 1 when not taken.
+int launch_decode_mfma_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                             const int8_t* w, const float* ws, int64_t N, const uint16_t* bias,
+                             uint16_t* y, int64_t ldy, int8_t* xq_out, float* xs_out,
+                             int32_t* acc_out, hipStream_t st);
 // Decode GEMM (M <= 64, pre-quantized activations) on MFMA; returns 1 when not taken.
 int launch_decode_mfma(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
                        const int8_t* w, const float* ws, int64_t N, const uint16_t* bias,

@@ -1,163 +1,103 @@
-// Decode GEMM for 4 < M <= 64 tokens on pre-quantized int8 activations (gfx950).
+// Decode GEMMs on MFMA (gfx950): int8 activations for 4 < M <= 64 tokens, and
+// fp16 activations quantized inside the kernel for M <= 4 (one launch per linear).
 //
-//   y[m, n] = fp16(((float)sum_k xq[m, k] * w[n, k]) * xs[m] * ws[n] (+ bias[n]))
+//   y[m, n] = fp16(((float)sum_k q[m, k] * w[n, k]) * s[m] * ws[n] (+ bias[n]))
 //
-// Still HBM-bound (the weight stream is N*K bytes against M*K of activations),
-// but with M up to 64 the products belong on MFMA.  Layout of the work:
+// HBM-bound: the weight stream is N*K bytes against M*K of activations.  What
+// limits these kernels on MI355X is the per-CU vector memory path (address
+// unit and L1), which spends a cycle per cache line touched: so every global
+// load instruction is laid out to cover whole 128-byte lines.  Layout:
 //   * A workgroup owns 16*NB weight rows; its WAVES waves split K into equal
 //     shares of 128-byte slabs.
-//   * Weights stream with the coalesced pattern of the decode GEMV: each wave
-//     load instruction covers 8 rows x 128 contiguous bytes (lane l: row l/8,
-//     bytes 16*(l%8) of the slab), non-temporal, register double-buffered one
-//     batch of SB slabs ahead.  That lane layout is not the MFMA operand
-//     layout, so every slab goes through a wave-private LDS tile (16-byte
-//     chunks XOR-swizzled by row, conflict-free both ways) and comes back as
-//     the B fragments of v_mfma_i32_16x16x64_i8 (lane l: row l%16, bytes
-//     16*(l/16) of a 64-byte half-slab).
-//   * The activation fragments (A operand, lane l: token l%16 of an MT tile,
-//     same bytes) are read from L2 and prefetched with the weights.
-//   * Two accumulator sets (one per half-slab) break the MFMA dependency
-//     chain; waves meet once at the end in an LDS reduction, then the fp16
-//     epilogue.
+//   * Weights: each wave load instruction covers 8 rows x 128 contiguous bytes
+//     (lane l: row l/8, bytes 16*(l%8) of the slab), non-temporal, register
+//     double-buffered one batch of SB slabs ahead.
+//   * int8 activations (decode_mfma_kernel) stream the same way: 8 tokens x
+//     128 bytes per instruction, prefetched with the weights.  Reading them in
+//     the MFMA operand layout instead (16 tokens x 64 bytes per instruction)
+//     touches twice the lines and measured 10-20% slower at M = 16..64.
+//   * Neither lane layout is the MFMA operand layout, so each slab goes through
+//     a wave-private LDS tile (16-byte chunks XOR-swizzled by row, conflict-free
+//     both ways) and comes back as the operands of v_mfma_i32_16x16x64_i8
+//     (lane l: row l%16, bytes 16*(l/16) of a 64-byte half-slab).
+//   * Two accumulator sets (one per half-slab) break the MFMA dependency chain;
+//     waves meet once at the end in an LDS reduction, then the fp16 epilogue.
 // Integer accumulation is exact, so the result does not depend on the K split.
+//
+// Fused quantization (decode_mfma_fused_kernel, M <= 4): every workgroup reads
+// the M fp16 rows of x (each wave its own K share, 1 KB per load instruction),
+// reduces each row's max magnitude (DPP, then one barrier across the waves),
+// and quantizes its share into a wave-private int8 area of LDS that feeds the
+// A operand for the whole K loop.  The loads of the first weight batch are
+// issued before all of this, so the quantization runs while they are in
+// flight.  Each workgroup quantizes the rows for itself (no workgroup waits
+// for another); on MFMA the dot products cost no VALU time, which is what made
+// the dot4 GEMV slow at M = 4.
 #include "common.h"
 
 namespace {
 
-__device__ __forceinline__ i32x4 ld16(const int8_t* p) {
+__device__ __forceinline__ i32x4 ld16(const void* p) {
     return *reinterpret_cast<const i32x4*>(p);
 }
 __device__ __forceinline__ i32x4 ld16_nt(const int8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
 }
 
-// 16-byte chunk position of (row, chunk) inside a 128-byte row of an LDS tile.
+// 16-byte chunk position of (row, chunk) inside a 128-byte row of an LDS tile:
+// rows r and r' with r = r' mod 4 get different chunk positions, so the 16
+// lanes of one ds_read_b128 pass (16 rows, one chunk) hit 16 distinct slots.
 __device__ __forceinline__ int swz(int row, int chunk) {
     return ((chunk ^ (row & 7) ^ ((row >> 3) & 7)) & 7) * 16;
 }
 
-template <int MT, int NB, int WAVES, int SB>
-__global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
-    const int8_t* __restrict__ xq, int64_t ldx, const float* __restrict__ xs, int M, int K,
-    const int8_t* __restrict__ w, const float* __restrict__ ws, int N,
-    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy,
-    int32_t* __restrict__ acc_out) {
-    constexpr int ROWS = 16 * NB;
-    constexpr int TILE = ROWS * 128;  // one slab of the wave's rows
-    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-    i32x4* red = reinterpret_cast<i32x4*>(smem);  // after the main loop: [WAVES][MT*NB][64]
+// Barrier that waits for LDS traffic only: the compiler's __syncthreads also
+// waits for every outstanding global load, which would drain the weight
+// prefetch.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * ROWS;
-    const int per = (K >> 7) / WAVES;  // slabs per wave (exact: the launcher checks)
-    const int s0 = wave * per, nb = per / SB;
-
-    // load side: lane -> (row rq + 8h, chunk c)
-    const int rq = lane >> 3, c = lane & 7;
-    const int8_t* wsrc[2 * NB];
+// Weight side of one wave: pointers and LDS offsets for the 2*NB load
+// instructions of a slab, and the B-fragment offsets for the MFMA.
+template <int NB>
+struct WeightLanes {
+    const int8_t* src[2 * NB];
     int woff[2 * NB];
-#pragma unroll
-    for (int h = 0; h < 2 * NB; h++) {
-        const int row = h * 8 + rq;
-        int n = n0 + row;
-        n = n < N ? n : N - 1;  // rows past N load real memory, never stored
-        wsrc[h] = w + (int64_t)n * K + (int64_t)s0 * 128 + c * 16;
-        woff[h] = row * 128 + swz(row, c);
-    }
-    // MFMA side: lane -> (row r, chunk 4q + g)
-    const int r = lane & 15, g = lane >> 4;
     int roff[NB][2];
+    __device__ __forceinline__ void init(const int8_t* w, int n0, int N, int64_t K, int s0,
+                                         int lane) {
+        const int rq = lane >> 3, c = lane & 7, r = lane & 15, g = lane >> 4;
 #pragma unroll
-    for (int b = 0; b < NB; b++)
-#pragma unroll
-        for (int q = 0; q < 2; q++) roff[b][q] = (b * 16 + r) * 128 + swz(b * 16 + r, 4 * q + g);
-    const int8_t* xrow[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++) {
-        int m = mt * 16 + r;
-        m = m < M ? m : M - 1;  // tokens past M compute into rows never stored
-        xrow[mt] = xq + (int64_t)m * ldx + (int64_t)s0 * 128 + g * 16;
-    }
-
-    i32x4 wa[SB][2 * NB], wb[SB][2 * NB];
-    i32x4 xa[SB][2][MT], xb[SB][2][MT];
-    auto load = [&](i32x4 (&dw)[SB][2 * NB], i32x4 (&dx)[SB][2][MT], int bt) {
-#pragma unroll
-        for (int j = 0; j < SB; j++)
-#pragma unroll
-            for (int h = 0; h < 2 * NB; h++) dw[j][h] = ld16_nt(wsrc[h] + (int64_t)(bt * SB + j) * 128);
-#pragma unroll
-        for (int j = 0; j < SB; j++)
-#pragma unroll
-            for (int q = 0; q < 2; q++)
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-                    dx[j][q][mt] = ld16(xrow[mt] + (int64_t)(bt * SB + j) * 128 + q * 64);
-    };
-    i32x4 acc[2][MT][NB];
-#pragma unroll
-    for (int q = 0; q < 2; q++)
-#pragma unroll
-        for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-            for (int b = 0; b < NB; b++) acc[q][mt][b] = i32x4{0, 0, 0, 0};
-
-    int8_t* st = smem + wave * (SB * TILE);
-    auto compute = [&](const i32x4 (&wv)[SB][2 * NB], const i32x4 (&ax)[SB][2][MT]) {
-        // The tile is private to the wave and LDS executes a wave's accesses in
-        // order; the barriers only keep the compiler from reordering across them.
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < SB; j++)
-#pragma unroll
-            for (int h = 0; h < 2 * NB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + woff[h]) = wv[j][h];
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < SB; j++) {
-            i32x4 bf[NB][2];
-#pragma unroll
-            for (int b = 0; b < NB; b++)
-#pragma unroll
-                for (int q = 0; q < 2; q++) bf[b][q] = *reinterpret_cast<const i32x4*>(st + j * TILE + roff[b][q]);
-#pragma unroll
-            for (int q = 0; q < 2; q++)
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-                    for (int b = 0; b < NB; b++)
-                        acc[q][mt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ax[j][q][mt], bf[b][q],
-                                                                             acc[q][mt][b], 0, 0, 0);
+        for (int h = 0; h < 2 * NB; h++) {
+            const int row = h * 8 + rq;
+            int n = n0 + row;
+            n = n < N ? n : N - 1;  // rows past N load real memory, never stored
+            src[h] = w + (int64_t)n * K + (int64_t)s0 * 128 + c * 16;
+            woff[h] = row * 128 + swz(row, c);
         }
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-    };
-    load(wa, xa, 0);
-    for (int bt = 0; bt < nb - 1; bt++) {
-        load(wb, xb, bt + 1);
-        compute(wa, xa);
 #pragma unroll
-        for (int j = 0; j < SB; j++) {
+        for (int b = 0; b < NB; b++)
 #pragma unroll
-            for (int h = 0; h < 2 * NB; h++) wa[j][h] = wb[j][h];
-#pragma unroll
-            for (int q = 0; q < 2; q++)
-#pragma unroll
-                for (int mt = 0; mt < MT; mt++) xa[j][q][mt] = xb[j][q][mt];
-        }
+            for (int q = 0; q < 2; q++) roff[b][q] = (b * 16 + r) * 128 + swz(b * 16 + r, 4 * q + g);
     }
-    compute(wa, xa);
+};
 
-    __syncthreads();  // the reduction area overlaps the tiles
+// Cross-wave reduction and epilogue shared by both kernels.  acc[q][mt][b]:
+// lane l, register i holds token mt*16 + 4*(l/16) + i, row b*16 + l%16.
+template <int MT, int NB, int WAVES>
+__device__ __forceinline__ void reduce_store(i32x4 (&acc)[2][MT][NB], i32x4* red, int wave,
+                                             int lane, int tid, int n0, int M, int N,
+                                             const float* xs, const float* __restrict__ ws,
+                                             const uint16_t* __restrict__ bias,
+                                             uint16_t* __restrict__ y, int64_t ldy,
+                                             int32_t* __restrict__ acc_out) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
         for (int b = 0; b < NB; b++)
             red[(wave * MT * NB + mt * NB + b) * 64 + lane] = acc[0][mt][b] + acc[1][mt][b];
     __syncthreads();
-    // result lane l, register i of block (mt, b): token mt*16 + 4*(l/16) + i, row b*16 + l%16
     for (int idx = tid; idx < MT * NB * 64; idx += WAVES * 64) {
         const int mb = idx >> 6, ln = idx & 63, mt = mb / NB, b = mb % NB;
         i32x4 s = red[mb * 64 + ln];
@@ -176,27 +116,320 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
     }
 }
 
+// ---- int8 activations, M <= 16*MT ------------------------------------------
+template <int MT, int NB, int WAVES, int SB>
+__global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
+    const int8_t* __restrict__ xq, int64_t ldx, const float* __restrict__ xs, int M, int K,
+    const int8_t* __restrict__ w, const float* __restrict__ ws, int N,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy,
+    int32_t* __restrict__ acc_out) {
+    constexpr int ROWS = 16 * NB;
+    constexpr int TROWS = ROWS + 16 * MT;  // weight rows, then token rows
+    constexpr int TILE = TROWS * 128;      // one slab of the wave's rows
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    i32x4* red = reinterpret_cast<i32x4*>(smem);  // after the main loop: [WAVES][MT*NB][64]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * ROWS;
+    const int per = (K >> 7) / WAVES;  // slabs per wave (exact: the launcher checks)
+    const int s0 = wave * per, nb = per / SB;
+    const int rq = lane >> 3, c = lane & 7, r = lane & 15, g = lane >> 4;
+
+    WeightLanes<NB> wl;
+    wl.init(w, n0, N, K, s0, lane);
+    // activation rows: load lane -> (token h*8 + rq, chunk c); tokens past M
+    // repeat token M-1 (computed, never stored)
+    const int8_t* xsrc[2 * MT];
+    int xwoff[2 * MT];
+#pragma unroll
+    for (int h = 0; h < 2 * MT; h++) {
+        const int tok = h * 8 + rq;
+        const int m = tok < M ? tok : M - 1;
+        xsrc[h] = xq + (int64_t)m * ldx + (int64_t)s0 * 128 + c * 16;
+        xwoff[h] = (ROWS + tok) * 128 + swz(tok, c);
+    }
+    int aoff[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int q = 0; q < 2; q++) aoff[mt][q] = (ROWS + mt * 16 + r) * 128 + swz(mt * 16 + r, 4 * q + g);
+
+    i32x4 wa[SB][2 * NB], wb[SB][2 * NB];
+    i32x4 xa[SB][2 * MT], xb[SB][2 * MT];
+    auto load = [&](i32x4 (&dw)[SB][2 * NB], i32x4 (&dx)[SB][2 * MT], int bt) {
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++) dw[j][h] = ld16_nt(wl.src[h] + (int64_t)(bt * SB + j) * 128);
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < 2 * MT; h++) dx[j][h] = ld16(xsrc[h] + (int64_t)(bt * SB + j) * 128);
+    };
+    i32x4 acc[2][MT][NB];
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+            for (int b = 0; b < NB; b++) acc[q][mt][b] = i32x4{0, 0, 0, 0};
+
+    int8_t* st = smem + wave * (SB * TILE);
+    auto compute = [&](const i32x4 (&wv)[SB][2 * NB], const i32x4 (&xv)[SB][2 * MT]) {
+        // The tile is private to the wave and LDS executes a wave's accesses in
+        // order; the barriers only keep the compiler from reordering across them.
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + wl.woff[h]) = wv[j][h];
+#pragma unroll
+            for (int h = 0; h < 2 * MT; h++) *reinterpret_cast<i32x4*>(st + j * TILE + xwoff[h]) = xv[j][h];
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+            i32x4 bf[NB][2], af[MT][2];
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) bf[b][q] = *reinterpret_cast<const i32x4*>(st + j * TILE + wl.roff[b][q]);
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) af[mt][q] = *reinterpret_cast<const i32x4*>(st + j * TILE + aoff[mt][q]);
+#pragma unroll
+            for (int q = 0; q < 2; q++)
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++) acc[q][mt][b] = fni8::mfma_i8(af[mt][q], bf[b][q], acc[q][mt][b]);
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    };
+    load(wa, xa, 0);
+    for (int bt = 0; bt < nb - 1; bt++) {
+        load(wb, xb, bt + 1);
+        compute(wa, xa);
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++) wa[j][h] = wb[j][h];
+#pragma unroll
+            for (int h = 0; h < 2 * MT; h++) xa[j][h] = xb[j][h];
+        }
+    }
+    compute(wa, xa);
+
+    __syncthreads();  // the reduction area overlaps the tiles
+    reduce_store<MT, NB, WAVES>(acc, red, wave, lane, tid, n0, M, N, xs, ws, bias, y, ldy, acc_out);
+}
+
+// ---- fp16 activations, M <= 4, quantized in the kernel ----------------------
+// PQ: each wave's K share is 4*PQ slabs (K = 512 * WAVES * PQ exactly), which
+// makes every loop trip count a compile-time constant.
+template <int NB, int WAVES, int SB, int PQ>
+__global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int M, int K, const int8_t* __restrict__ w,
+    const float* __restrict__ ws, int N, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ y, int64_t ldy, int8_t* __restrict__ xq_out,
+    float* __restrict__ xs_out, int32_t* __restrict__ acc_out) {
+    constexpr int ROWS = 16 * NB;
+    constexpr int TILE = ROWS * 128;
+    constexpr int PER = 4 * PQ;           // slabs per wave
+    constexpr int NBT = PER / SB;         // batches per wave
+    constexpr int XAREA = PER * 4 * 128;  // the wave's int8 activations: [PER][4 tokens][128]
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int8_t* tiles = smem;                                     // [WAVES][SB][TILE]
+    int8_t* xarea = smem + WAVES * SB * TILE;                 // [WAVES][XAREA]
+    uint32_t* amx = reinterpret_cast<uint32_t*>(xarea + WAVES * XAREA);  // [WAVES][4]
+    float* scl = reinterpret_cast<float*>(amx + WAVES * 4);   // [4]
+    i32x4* red = reinterpret_cast<i32x4*>(smem);              // after the main loop
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * ROWS;
+    const int s0 = wave * PER;
+    const int r = lane & 15, g = lane >> 4;
+
+    // 1. activation loads first (the compiler then waits for them without
+    //    waiting for the weight loads issued after): chunk j of this lane is
+    //    token j / PQ, elements s0*128 + ((j % PQ) * 64 + lane) * 8 .. + 8.
+    uint4 xv[4 * PQ];
+#pragma unroll
+    for (int j = 0; j < 4 * PQ; j++) {
+        const int m = j / PQ;
+        if (m < M)
+            xv[j] = *reinterpret_cast<const uint4*>(
+                x + (int64_t)m * ldx + (int64_t)s0 * 128 + ((j % PQ) * 64 + lane) * 8);
+        else
+            xv[j] = make_uint4(0, 0, 0, 0);
+    }
+    // 2. first weight batch
+    WeightLanes<NB> wl;
+    wl.init(w, n0, N, K, s0, lane);
+    i32x4 wa[SB][2 * NB], wb[SB][2 * NB];
+#pragma unroll
+    for (int j = 0; j < SB; j++)
+#pragma unroll
+        for (int h = 0; h < 2 * NB; h++) wa[j][h] = ld16_nt(wl.src[h] + (int64_t)j * 128);
+
+    // 3. row max magnitudes: integer max over (bits & 0x7fff), one wave-uniform
+    //    value per token, then across the waves
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        uint32_t mx = 0;
+#pragma unroll
+        for (int jj = 0; jj < PQ; jj++) {
+            const uint4 v = xv[m * PQ + jj];
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t lo = w4[e] & 0x7fffu, hi = (w4[e] >> 16) & 0x7fffu;
+                mx = lo > mx ? lo : mx;
+                mx = hi > mx ? hi : mx;
+            }
+        }
+        mx = fni8::wave_max_uniform(mx);
+        if (lane == 0) amx[wave * 4 + m] = mx;
+    }
+    lds_barrier();
+    float sc[4], yr[4];
+    bool live[4];
+#pragma unroll
+    for (int m = 0; m < 4; m++) {
+        uint32_t a = amx[m];
+#pragma unroll
+        for (int wv = 1; wv < WAVES; wv++) a = amx[wv * 4 + m] > a ? amx[wv * 4 + m] : a;
+        sc[m] = fni8::row_scale_from_bits(a);
+        live[m] = m < M && __builtin_isfinite(sc[m]);  // NaN/inf scale: every q is 0
+        yr[m] = 1.0f / sc[m];                          // correctly rounded (build flag)
+    }
+    if (wave == 0 && lane < 4) {
+        scl[lane] = lane == 0 ? sc[0] : lane == 1 ? sc[1] : lane == 2 ? sc[2] : sc[3];
+        if (blockIdx.x == 0 && lane < M) xs_out[lane] = scl[lane];
+    }
+    // 4. quantize this wave's share into its LDS area (token rows of 128 bytes
+    //    per slab; rows of different tokens are 128 bytes apart, so the A-operand
+    //    reads below are conflict-free without a swizzle)
+    int8_t* xw = xarea + wave * XAREA;
+#pragma unroll
+    for (int j = 0; j < 4 * PQ; j++) {
+        const int m = j / PQ;
+        if (m >= M) continue;
+        const int kl = ((j % PQ) * 64 + lane) * 8;  // element offset in the share
+        const uint2 q = fni8::quant_chunk(xv[j], sc[m], yr[m], live[m]);
+        *reinterpret_cast<uint2*>(xw + ((kl >> 7) * 4 + m) * 128 + (kl & 127)) = q;
+        if (blockIdx.x == 0)
+            *reinterpret_cast<uint2*>(xq_out + (int64_t)m * K + (int64_t)s0 * 128 + kl) = q;
+    }
+    const int tok = r < M ? r : M - 1;  // tokens past M repeat M-1 (never stored)
+    int aoff[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) aoff[q] = tok * 128 + q * 64 + g * 16;
+
+    // 5. the weight stream
+    i32x4 acc[2][1][NB];
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[q][0][b] = i32x4{0, 0, 0, 0};
+    int8_t* st = tiles + wave * (SB * TILE);
+    auto compute = [&](const i32x4 (&wv)[SB][2 * NB], int bt) {
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + wl.woff[h]) = wv[j][h];
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+            const int8_t* xs_ = xw + (bt * SB + j) * 512;
+            const i32x4 a0 = ld16(xs_ + aoff[0]), a1 = ld16(xs_ + aoff[1]);
+            i32x4 bf[NB][2];
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) bf[b][q] = *reinterpret_cast<const i32x4*>(st + j * TILE + wl.roff[b][q]);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                acc[0][0][b] = fni8::mfma_i8(a0, bf[b][0], acc[0][0][b]);
+                acc[1][0][b] = fni8::mfma_i8(a1, bf[b][1], acc[1][0][b]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    };
+#pragma unroll
+    for (int bt = 0; bt < NBT - 1; bt++) {
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)((bt + 1) * SB + j) * 128);
+        compute(wa, bt);
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++) wa[j][h] = wb[j][h];
+    }
+    compute(wa, NBT - 1);
+
+    __syncthreads();  // the reduction area overlaps the tiles
+    reduce_store<1, NB, WAVES>(acc, red, wave, lane, tid, n0, M, N, scl, ws, bias, y, ldy, acc_out);
+}
+
 template <int MT, int NB, int WAVES, int SB>
 int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const int8_t* w,
            const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
            int32_t* acc_out, hipStream_t st) {
     const int slabs = K >> 7;
     if (slabs % WAVES != 0 || (slabs / WAVES) % SB != 0) return 1;
-    constexpr size_t tiles = (size_t)WAVES * SB * 16 * NB * 128;
+    constexpr size_t tiles = (size_t)WAVES * SB * (16 * NB + 16 * MT) * 128;
     constexpr size_t red = (size_t)WAVES * MT * NB * 64 * 16;
     constexpr size_t lds = tiles > red ? tiles : red;
-    static_assert(lds <= 64 * 1024, "decode GEMM LDS budget");
-    hipLaunchKernelGGL((decode_mfma_kernel<MT, NB, WAVES, SB>),
-                       dim3((unsigned)((N + 16 * NB - 1) / (16 * NB))), dim3(WAVES * 64), lds, st,
-                       xq, ldx, xs, M, K, w, ws, N, bias, y, ldy, acc_out);
+    static_assert(lds <= 160 * 1024, "decode GEMM LDS budget");
+    auto kern = decode_mfma_kernel<MT, NB, WAVES, SB>;
+    if constexpr (lds > 64 * 1024) {
+        static const bool ok = hipFuncSetAttribute((const void*)kern,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)lds) == hipSuccess;
+        if (!ok) return 1;
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * NB - 1) / (16 * NB))), dim3(WAVES * 64), lds,
+                       st, xq, ldx, xs, M, K, w, ws, N, bias, y, ldy, acc_out);
+    return FNI8_OK;
+}
+
+template <int NB, int WAVES, int SB, int PQ>
+int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, const float* ws,
+                 int N, const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
+                 float* xs_out, int32_t* acc_out, hipStream_t st) {
+    static_assert((4 * PQ) % SB == 0, "batches must divide the share");
+    if (K != 512 * WAVES * PQ) return 1;
+    constexpr size_t tiles = (size_t)WAVES * SB * 16 * NB * 128;
+    const size_t lds_main = tiles + (size_t)WAVES * 4 * PQ * 512 + WAVES * 16 + 16;
+    constexpr size_t red = (size_t)WAVES * NB * 64 * 16;
+    const size_t lds = lds_main > red ? lds_main : red;
+    if (lds > 160 * 1024) return 1;
+    auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ>;
+    static const bool ok = hipFuncSetAttribute((const void*)kern,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               160 * 1024) == hipSuccess;
+    if (!ok) return 1;
+    hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * NB - 1) / (16 * NB))), dim3(WAVES * 64), lds,
+                       st, x, ldx, M, K, w, ws, N, bias, y, ldy, xq_out, xs_out, acc_out);
     return FNI8_OK;
 }
 
 // Launch shapes by M tile and weight shape, measured on MI355X over the
-// Qwen3-8B decode linears (36 distinct weight copies, weights from HBM):
-// wide N takes 32/64-row workgroups (activation fragments reused across row
-// blocks), long K and narrow N 8 waves over 16 rows.  Other shapes take the
-// first generic entry whose wave split divides K.
+// Qwen3-8B decode linears (36 distinct weight copies, weights from HBM).
+// Other shapes take the first generic entry whose wave split divides K.
 template <int MT>
 int launch_mt(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const int8_t* w,
               const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
@@ -210,22 +443,56 @@ int launch_mt(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, cons
     const bool wide = N >= 16384, longk = K >= 8192, narrow = N <= 4096;
     if constexpr (MT == 1) {
         if (wide) FNI8_DM(2, 4, 1);
-        else if (longk || narrow) FNI8_DM(1, 8, 1);
+        else if (longk) FNI8_DM(1, 8, 2);
+        else if (narrow) FNI8_DM(1, 4, 2);
         else FNI8_DM(2, 4, 2);
     } else if constexpr (MT == 2) {
         if (wide) FNI8_DM(2, 4, 1);
         else if (longk || narrow) FNI8_DM(1, 4, 2);
         else FNI8_DM(2, 8, 1);
     } else {
-        if (wide) FNI8_DM(4, 4, 1);
+        if (wide) FNI8_DM(2, 8, 1);
         else if (longk) FNI8_DM(1, 4, 1);
         else if (narrow) FNI8_DM(1, 8, 1);
-        else FNI8_DM(2, 4, 1);
+        else FNI8_DM(2, 8, 1);
     }
     FNI8_DM(1, 4, 1);
     FNI8_DM(1, 2, 1);
     FNI8_DM(1, 1, 1);
 #undef FNI8_DM
+    return 1;
+}
+
+int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w,
+                       const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
+                       int8_t* xq_out, float* xs_out, int32_t* acc_out, hipStream_t st) {
+#define FNI8_DF(NB, WV, SB, PQ)                                                                 \
+    do {                                                                                        \
+        const int rc = launch_fused<NB, WV, SB, PQ>(x, ldx, M, K, w, ws, N, bias, y, ldy,       \
+                                                    xq_out, xs_out, acc_out, st);               \
+        if (rc != 1) return rc;                                                                 \
+    } while (0)
+    const bool wide = N >= 16384, narrow = N <= 4096;
+    if (wide) {
+        FNI8_DF(2, 4, 2, 2);
+        FNI8_DF(2, 8, 1, 3);
+    } else if (narrow) {
+        FNI8_DF(1, 4, 4, 2);
+        FNI8_DF(1, 8, 3, 3);
+    } else {
+        FNI8_DF(2, 8, 1, 1);
+        FNI8_DF(2, 8, 1, 3);
+    }
+    // generic entries: K = 1024, 2048, 3072, 4096, 5120, 6144, 8192, 12288
+    FNI8_DF(1, 2, 2, 1);
+    FNI8_DF(1, 4, 2, 1);
+    FNI8_DF(1, 2, 2, 3);
+    FNI8_DF(1, 8, 2, 1);
+    FNI8_DF(1, 2, 2, 5);
+    FNI8_DF(1, 4, 2, 3);
+    FNI8_DF(1, 8, 2, 2);
+    FNI8_DF(1, 8, 1, 3);
+#undef FNI8_DF
     return 1;
 }
 
@@ -245,6 +512,28 @@ int launch_decode_mfma(const int8_t* xq, int64_t ldq, const float* xs, int64_t M
     if (M <= 16) return launch_mt<1>(xq, ldq, xs, m, k, w, ws, n, bias, y, ldy, acc_out, st);
     if (M <= 32) return launch_mt<2>(xq, ldq, xs, m, k, w, ws, n, bias, y, ldy, acc_out, st);
     return launch_mt<4>(xq, ldq, xs, m, k, w, ws, n, bias, y, ldy, acc_out, st);
+}
+
+// fp16 activations, M <= 4, quantization fused: returns 1 when the shape is
+// not taken (K not 512 * waves * PQ for a table entry, misaligned operands).
+// xq_out (row stride K) and xs_out receive the quantized activations.
+int launch_decode_mfma_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                             const int8_t* w, const float* ws, int64_t N, const uint16_t* bias,
+                             uint16_t* y, int64_t ldy, int8_t* xq_out, float* xs_out,
+                             int32_t* acc_out, hipStream_t st) {
+    if (M < 1 || M > 4 || K % 512 != 0 || ldx % 8 != 0 || (uintptr_t)x % 16 != 0 ||
+        (uintptr_t)w % 16 != 0 || xq_out == nullptr || xs_out == nullptr ||
+        (uintptr_t)xq_out % 8 != 0)
+        return 1;
+    const int rc = launch_fused_table(x, ldx, (int)M, (int)K, w, ws, (int)N, bias, y, ldy, xq_out,
+                                      xs_out, acc_out, st);
+    if (rc != FNI8_OK) return rc;
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error_detail("decode launch: %s", hipGetErrorString(e));
+        return FNI8_ERR_LAUNCH;
+    }
+    return FNI8_OK;
 }
 
 }  // namespace fni8h

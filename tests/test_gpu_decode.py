@@ -1,6 +1,8 @@
 """GPU parity of the decode path: for M <= 4 the single-launch linear with the
-per-token quantization fused into the GEMV (and the same GEMV on pre-quantized
-activations); for 4 < M <= 64 the quantize launch plus the MFMA decode GEMM.
+per-token quantization fused into the GEMM (the dot4 GEMV for M <= 2, the MFMA
+kernel for M = 3..4 where K is one of its shapes, else the GEMV), and the same
+GEMV on pre-quantized activations; for 4 < M <= 64 the quantize launch plus the
+MFMA decode GEMM.
 
 Bar: int8 activations, fp32 scales, int32 accumulators and fp16 outputs are
 bit-identical to the CPU oracle on the same seeded inputs.  The fused kernel
@@ -76,6 +78,10 @@ def test_prequantized_decode_gemm_bitexact(pkg, wl, cuda, name, M):
     (4, 6144, 8192),   # long K: 8 waves
     (2, 4096, 12288),
     (3, 40, 64),       # K % 128 != 0 -> two-launch path
+    (4, 72, 2048),     # MFMA fused, 4 waves x 4 slabs; N not a multiple of 16
+    (3, 24, 3072),     # MFMA fused, 2 waves x 12 slabs
+    (4, 520, 5120),    # MFMA fused, 2 waves x 20 slabs
+    (4, 33, 1536),     # K not 512 * waves * PQ for any entry -> GEMV
 ])
 def test_fused_ragged_bitexact(pkg, wl, cuda, M, N, K):
     x = wl.activations(M, K, seed=M * 13 + K)
@@ -154,10 +160,12 @@ def test_fused_quant_exhaustive_fp16(pkg, cuda):
             assert np.array_equal(acc.cpu().numpy()[:, 0], xqr.astype(np.int64).sum(1))
 
 
-def test_fused_graph_replay(pkg, wl, cuda):
-    """The fused decode launch captured in a HIP graph equals eager on every replay."""
+@pytest.mark.parametrize("M", [2, 4])
+def test_fused_graph_replay(pkg, wl, cuda, M):
+    """The fused decode launch (GEMV at M=2, MFMA at M=4) captured in a HIP graph
+    equals eager on every replay."""
     qt = pkg.QTensor(*[t.cuda() for t in wl.weight_i8(4096, 4096, seed=71)], scheme="per_row_i8")
-    static_x = wl.activations(2, 4096, seed=72).cuda()
+    static_x = wl.activations(M, 4096, seed=72).cuda()
     for _ in range(3):
         pkg.linear(static_x, qt)
     torch.cuda.synchronize()
@@ -165,7 +173,7 @@ def test_fused_graph_replay(pkg, wl, cuda):
     with torch.cuda.graph(g):
         static_y = pkg.linear(static_x, qt)
     for i in range(4):
-        xi = wl.activations(2, 4096, seed=80 + i).cuda()
+        xi = wl.activations(M, 4096, seed=80 + i).cuda()
         static_x.copy_(xi)
         g.replay()
         eager = pkg.linear(xi, qt)
