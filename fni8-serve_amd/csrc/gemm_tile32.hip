@@ -296,21 +296,50 @@ int launch_tile32(const int8_t* aq, int64_t lda, const float* as, const int32_t*
         return launch<128, 256, 64, true>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off, bias,
                                           y, ldy, acc_out, slots, st);
     }
-    // Dense: the biggest tile that still fills the 256 CUs in whole rounds.
-    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
-    const double fill256 = (double)t256 / (double)(((t256 + 255) / 256) * 256);
-    if (t256 >= 256 && fill256 >= 0.7) {
-        if (k128)
-            return launch<256, 256, 128, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
-                                                bias, y, ldy, acc_out, 0, st);
-        return launch<256, 256, 64, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
-                                           bias, y, ldy, acc_out, 0, st);
+    // Dense: the tile whose workgroups fill the CUs best in whole rounds (one
+    // workgroup per CU at a time: the LDS stages take most of the 160 KB);
+    // ties go to the bigger tile, which reads fewer bytes per MFMA op.  On the
+    // Qwen3-8B shapes at M = 512..4096 this picks the fastest of the six
+    // measured tiles in every case.
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        return n;
+    }();
+    constexpr int kTiles[6][2] = {{256, 256}, {128, 256}, {256, 128}, {128, 128}, {64, 256}, {64, 128}};
+    int best = 0;
+    double best_fill = -1.0;
+    for (int i = 0; i < 6; i++) {
+        const int64_t wgs = ((M + kTiles[i][0] - 1) / kTiles[i][0]) * ((N + kTiles[i][1] - 1) / kTiles[i][1]);
+        const double fill = (double)wgs / (double)(((wgs + cus - 1) / cus) * cus);
+        if (fill > best_fill + 1e-9) {
+            best_fill = fill;
+            best = i;
+        }
     }
-    if (k128)
-        return launch<128, 256, 128, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
-                                            bias, y, ldy, acc_out, 0, st);
-    return launch<128, 256, 64, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off, bias, y,
-                                       ldy, acc_out, 0, st);
+#define FNI8_T32(BM, BN)                                                                          \
+    return k128 ? launch<BM, BN, 128, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,  \
+                                             bias, y, ldy, acc_out, 0, st)                        \
+                : launch<BM, BN, 64, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,   \
+                                            bias, y, ldy, acc_out, 0, st)
+#define FNI8_T32_K128(BM, BN)                                                                     \
+    return launch<BM, BN, 128, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off, bias, y,  \
+                                      ldy, acc_out, 0, st)
+    // 64-row tiles need 128-byte K steps (one 16-byte chunk per thread and operand)
+    if (!k128 && best >= 4) best = 3;
+    switch (best) {
+        case 0: FNI8_T32(256, 256);
+        case 1: FNI8_T32(128, 256);
+        case 2: FNI8_T32(256, 128);
+        case 3: FNI8_T32(128, 128);
+        case 4: FNI8_T32_K128(64, 256);
+        default: FNI8_T32_K128(64, 128);
+    }
+#undef FNI8_T32_K128
+#undef FNI8_T32
 }
 
 }  // namespace fni8h
