@@ -217,6 +217,13 @@ int launch_decode_mfma_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t 
                              const int8_t* w, const float* ws, int64_t N, const uint16_t* bias,
                              uint16_t* y, int64_t ldy, int8_t* xq_out, float* xs_out,
                              int32_t* acc_out, hipStream_t st);
+// Grouped expert GEMM on MFMA for small segments (<= 48 rows per expert on
+// average); returns 1 when not taken.
+int launch_decode_mfma_grouped(const int8_t* aq, int64_t lda, const float* as,
+                               const int32_t* row_index, int64_t R_max, int64_t K,
+                               const int8_t* w, const float* ws, int64_t E, int64_t N,
+                               const int32_t* seg_off, const uint16_t* bias, uint16_t* y,
+                               int64_t ldy, int32_t* acc_out, hipStream_t st);
 // Decode GEMM (M <= 64, pre-quantized activations) on MFMA; returns 1 when not taken.
 int launch_decode_mfma(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
                        const int8_t* w, const float* ws, int64_t N, const uint16_t* bias,

@@ -85,10 +85,13 @@ struct WeightLanes {
 
 // Cross-wave reduction and epilogue shared by both kernels.  acc[q][mt][b]:
 // lane l, register i holds token mt*16 + 4*(l/16) + i, row b*16 + l%16.
+// Token m of the tile is output row r0 + m; its activation scale is
+// xs[rmap[r0 + m]] (xs[r0 + m] without a row map).
 template <int MT, int NB, int WAVES>
 __device__ __forceinline__ void reduce_store(i32x4 (&acc)[2][MT][NB], i32x4* red, int wave,
-                                             int lane, int tid, int n0, int M, int N,
-                                             const float* xs, const float* __restrict__ ws,
+                                             int lane, int tid, int n0, int r0, int M, int N,
+                                             const float* xs, const int32_t* __restrict__ rmap,
+                                             const float* __restrict__ ws,
                                              const uint16_t* __restrict__ bias,
                                              uint16_t* __restrict__ y, int64_t ldy,
                                              int32_t* __restrict__ acc_out) {
@@ -110,17 +113,24 @@ __device__ __forceinline__ void reduce_store(i32x4 (&acc)[2][MT][NB], i32x4* red
         for (int i = 0; i < 4; i++) {
             const int m = mt * 16 + (ln >> 4) * 4 + i;
             if (m >= M) continue;
-            y[(int64_t)m * ldy + col] = fni8::dequant_one(s[i], xs[m], wsc, bias, col);
-            if (acc_out != nullptr) acc_out[(int64_t)m * N + col] = s[i];
+            const int row = r0 + m;
+            const float xsc = xs[rmap != nullptr ? rmap[row] : row];
+            y[(int64_t)row * ldy + col] = fni8::dequant_one(s[i], xsc, wsc, bias, col);
+            if (acc_out != nullptr) acc_out[(int64_t)row * N + col] = s[i];
         }
     }
 }
 
 // ---- int8 activations, M <= 16*MT ------------------------------------------
-template <int MT, int NB, int WAVES, int SB>
+// GROUPED: the expert-segment form of the MoE layer (segments seg_off[E+1] of
+// sorted rows; tile slot blockIdx.x is one 16*MT-row piece of one expert's
+// segment, blockIdx.y the weight-row block; sorted row r reads activation row
+// rmap[r]; weights, scales and bias are stacked per expert).
+template <int MT, int NB, int WAVES, int SB, bool GROUPED>
 __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
-    const int8_t* __restrict__ xq, int64_t ldx, const float* __restrict__ xs, int M, int K,
-    const int8_t* __restrict__ w, const float* __restrict__ ws, int N,
+    const int8_t* __restrict__ xq, int64_t ldx, const float* __restrict__ xs,
+    const int32_t* __restrict__ rmap, int M, int K, const int8_t* __restrict__ w,
+    const float* __restrict__ ws, int N, int E, const int32_t* __restrict__ seg_off,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy,
     int32_t* __restrict__ acc_out) {
     constexpr int ROWS = 16 * NB;
@@ -131,7 +141,20 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * ROWS;
+    int n0, r0 = 0;
+    if constexpr (GROUPED) {
+        // every wave finds the same tile; past the last tile the whole
+        // workgroup leaves before any barrier
+        int e, r1;
+        if (!fni8::find_group_tile(seg_off, E, 16 * MT, blockIdx.x, e, r0, r1)) return;
+        M = r1 - r0;
+        n0 = blockIdx.y * ROWS;
+        w += (int64_t)e * N * K;
+        ws += (int64_t)e * N;
+        if (bias != nullptr) bias += (int64_t)e * N;
+    } else {
+        n0 = blockIdx.x * ROWS;
+    }
     const int per = (K >> 7) / WAVES;  // slabs per wave (exact: the launcher checks)
     const int s0 = wave * per, nb = per / SB;
     const int rq = lane >> 3, c = lane & 7, r = lane & 15, g = lane >> 4;
@@ -145,8 +168,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
 #pragma unroll
     for (int h = 0; h < 2 * MT; h++) {
         const int tok = h * 8 + rq;
-        const int m = tok < M ? tok : M - 1;
-        xsrc[h] = xq + (int64_t)m * ldx + (int64_t)s0 * 128 + c * 16;
+        const int row = r0 + (tok < M ? tok : M - 1);
+        const int src = (GROUPED && rmap != nullptr) ? rmap[row] : row;
+        xsrc[h] = xq + (int64_t)src * ldx + (int64_t)s0 * 128 + c * 16;
         xwoff[h] = (ROWS + tok) * 128 + swz(tok, c);
     }
     int aoff[MT][2];
@@ -226,7 +250,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
     compute(wa, xa);
 
     __syncthreads();  // the reduction area overlaps the tiles
-    reduce_store<MT, NB, WAVES>(acc, red, wave, lane, tid, n0, M, N, xs, ws, bias, y, ldy, acc_out);
+    reduce_store<MT, NB, WAVES>(acc, red, wave, lane, tid, n0, r0, M, N, xs,
+                                GROUPED ? rmap : nullptr, ws, bias, y, ldy, acc_out);
 }
 
 // ---- fp16 activations, M <= 4, quantized in the kernel ----------------------
@@ -381,28 +406,34 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     compute(wa, NBT - 1);
 
     __syncthreads();  // the reduction area overlaps the tiles
-    reduce_store<1, NB, WAVES>(acc, red, wave, lane, tid, n0, M, N, scl, ws, bias, y, ldy, acc_out);
+    reduce_store<1, NB, WAVES>(acc, red, wave, lane, tid, n0, 0, M, N, scl, nullptr, ws, bias, y,
+                               ldy, acc_out);
 }
 
-template <int MT, int NB, int WAVES, int SB>
+template <int MT, int NB, int WAVES, int SB, bool GROUPED = false>
 int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const int8_t* w,
            const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
-           int32_t* acc_out, hipStream_t st) {
+           int32_t* acc_out, hipStream_t st, const int32_t* rmap = nullptr, int E = 0,
+           const int32_t* seg_off = nullptr) {
     const int slabs = K >> 7;
     if (slabs % WAVES != 0 || (slabs / WAVES) % SB != 0) return 1;
     constexpr size_t tiles = (size_t)WAVES * SB * (16 * NB + 16 * MT) * 128;
     constexpr size_t red = (size_t)WAVES * MT * NB * 64 * 16;
     constexpr size_t lds = tiles > red ? tiles : red;
     static_assert(lds <= 160 * 1024, "decode GEMM LDS budget");
-    auto kern = decode_mfma_kernel<MT, NB, WAVES, SB>;
+    auto kern = decode_mfma_kernel<MT, NB, WAVES, SB, GROUPED>;
     if constexpr (lds > 64 * 1024) {
         static const bool ok = hipFuncSetAttribute((const void*)kern,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    (int)lds) == hipSuccess;
         if (!ok) return 1;
     }
-    hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * NB - 1) / (16 * NB))), dim3(WAVES * 64), lds,
-                       st, xq, ldx, xs, M, K, w, ws, N, bias, y, ldy, acc_out);
+    const unsigned nblk = (unsigned)((N + 16 * NB - 1) / (16 * NB));
+    // grouped: one slot per 16*MT-row piece of a segment; at most
+    // ceil(M / (16*MT)) + E of them are non-empty
+    const dim3 grid = GROUPED ? dim3((unsigned)((M + 16 * MT - 1) / (16 * MT) + E), nblk) : dim3(nblk);
+    hipLaunchKernelGGL(kern, grid, dim3(WAVES * 64), lds, st, xq, ldx, xs, rmap, M, K, w, ws, N, E,
+                       seg_off, bias, y, ldy, acc_out);
     return FNI8_OK;
 }
 
@@ -463,6 +494,28 @@ int launch_mt(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, cons
     return 1;
 }
 
+// Grouped (MoE) shapes: 2-wave workgroups over 32 weight rows measured fastest
+// on the 128-expert top-8 routing (gate_up 1536x2048, down 2048x768) at
+// T = 16 and 256, ahead of 4- and 8-wave splits.
+template <int MT>
+int launch_grouped_mt(const int8_t* xq, int64_t ldx, const float* xs, const int32_t* rmap, int R,
+                      int K, const int8_t* w, const float* ws, int E, int N,
+                      const int32_t* seg_off, const uint16_t* bias, uint16_t* y, int64_t ldy,
+                      int32_t* acc_out, hipStream_t st) {
+#define FNI8_DG(NB, WV, SB)                                                                     \
+    do {                                                                                        \
+        const int rc = launch<MT, NB, WV, SB, true>(xq, ldx, xs, R, K, w, ws, N, bias, y, ldy,  \
+                                                    acc_out, st, rmap, E, seg_off);             \
+        if (rc != 1) return rc;                                                                 \
+    } while (0)
+    FNI8_DG(2, 2, 1);
+    FNI8_DG(1, 2, 1);
+    FNI8_DG(2, 1, 1);
+    FNI8_DG(1, 1, 1);
+#undef FNI8_DG
+    return 1;
+}
+
 int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w,
                        const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
                        int8_t* xq_out, float* xs_out, int32_t* acc_out, hipStream_t st) {
@@ -512,6 +565,29 @@ int launch_decode_mfma(const int8_t* xq, int64_t ldq, const float* xs, int64_t M
     if (M <= 16) return launch_mt<1>(xq, ldq, xs, m, k, w, ws, n, bias, y, ldy, acc_out, st);
     if (M <= 32) return launch_mt<2>(xq, ldq, xs, m, k, w, ws, n, bias, y, ldy, acc_out, st);
     return launch_mt<4>(xq, ldq, xs, m, k, w, ws, n, bias, y, ldy, acc_out, st);
+}
+
+// Grouped expert GEMM (MoE) on MFMA for small segments: returns 1 when not
+// taken (more than 48 rows per expert on average, K % 128 != 0, misaligned
+// operands), so the caller uses the tile kernel.  The tile height follows the
+// average segment: 16 rows up to 8 rows per expert, else 32 (64-row tiles
+// measured 1.5-2x slower on skewed routings: most segments are small).
+int launch_decode_mfma_grouped(const int8_t* aq, int64_t lda, const float* as,
+                               const int32_t* row_index, int64_t R_max, int64_t K,
+                               const int8_t* w, const float* ws, int64_t E, int64_t N,
+                               const int32_t* seg_off, const uint16_t* bias, uint16_t* y,
+                               int64_t ldy, int32_t* acc_out, hipStream_t st) {
+    if (R_max < 1 || E < 1 || K % 128 != 0 || lda % 16 != 0 || (uintptr_t)aq % 16 != 0 ||
+        (uintptr_t)w % 16 != 0)
+        return 1;
+    const double avg = (double)R_max / (double)E;
+    if (avg > 48.0) return 1;
+    const int r = (int)R_max, k = (int)K, e = (int)E, n = (int)N;
+    if (avg <= 8.0)
+        return launch_grouped_mt<1>(aq, lda, as, row_index, r, k, w, ws, e, n, seg_off, bias, y,
+                                    ldy, acc_out, st);
+    return launch_grouped_mt<2>(aq, lda, as, row_index, r, k, w, ws, e, n, seg_off, bias, y, ldy,
+                                acc_out, st);
 }
 
 // fp16 activations, M <= 4, quantization fused: returns 1 when the shape is

@@ -462,12 +462,19 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
     if (!fast) {
         if (grouped) launch_generic<true>(a, st); else launch_generic<false>(a, st);
     } else if (grouped) {
-        // Expert segments: average rows per expert picks the kernel.
+        // Expert segments: average rows per expert picks the kernel -- the MFMA
+        // decode kernel in grouped form for small segments (the skinny kernel
+        // where it does not take the shape), the tile kernel for large ones.
         const double avg = (double)M / (double)E;
         if (avg <= 48.0) {
-            const unsigned slots = (unsigned)((M + 15) / 16 + E);
-            if (K >= 1024) launch_skinny<1, 1, 4, 8, true>(a, slots, st);
-            else launch_skinny<1, 1, 2, 8, true>(a, slots, st);
+            rc = launch_decode_mfma_grouped(aq, lda, as, row_index, M, K, w, ws, E, N, seg_off,
+                                            bias, y, ldy, acc_out, st);
+            if (rc == 1) {
+                rc = FNI8_OK;
+                const unsigned slots = (unsigned)((M + 15) / 16 + E);
+                if (K >= 1024) launch_skinny<1, 1, 4, 8, true>(a, slots, st);
+                else launch_skinny<1, 1, 2, 8, true>(a, slots, st);
+            }
         } else {
             rc = launch_tile32(aq, lda, as, row_index, M, K, w, ws, N, E, seg_off, bias, y, ldy,
                                acc_out, st);

@@ -83,6 +83,36 @@ def test_grouped_gemm_bitexact(pkg, wl, cuda, T, proj):
         assert np.array_equal(y.cpu().numpy()[rows].view(np.uint16), ys.view(np.uint16))
 
 
+@pytest.mark.parametrize("sizes,N,K", [
+    ([0, 1, 5, 0, 3, 2, 0, 1], 200, 768),        # ~1.5 rows/expert: 16-row tiles, 2-wave K split
+    ([0, 70, 1, 17, 33, 0, 2, 4], 1536, 2048),   # ~16 rows/expert: 32-row tiles, a 3-tile segment
+    ([40, 0, 64, 65, 1, 30, 48, 63], 104, 1024),  # ~39 rows/expert: 32-row tiles, N % 32 != 0
+])
+@pytest.mark.parametrize("gather", [False, True])
+def test_grouped_mfma_segments_bitexact(pkg, wl, cuda, sizes, N, K, gather):
+    """Skewed expert segments (empty, single-row, multi-tile) through the grouped
+    MFMA kernel, with bias and, optionally, a token gather by row index."""
+    E = len(sizes)
+    seg_r = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    R = int(seg_r[-1])
+    rng = np.random.default_rng(R + N + K)
+    w, ws = wl.expert_weights(E, N, K, seed=R + 7)
+    bias = torch.from_numpy((rng.standard_normal((E, N)) * 3).astype(np.float16))
+    A = R + 11 if gather else R
+    x = wl.activations(A, K, seed=R + 3)
+    aq, as_ = pkg.quantize_rowwise(x.cuda())
+    ri = rng.integers(0, A, R).astype(np.int32) if gather else None
+    y, acc = pkg.gemm_w8a8_grouped(aq, as_, w.cuda(), ws.cuda(), torch.from_numpy(seg_r).cuda(), R,
+                                   row_index=None if ri is None else torch.from_numpy(ri).cuda(),
+                                   bias=bias.cuda(), want_acc=True)
+    torch.cuda.synchronize()
+    aq_r, as_r = oracle.quant_rowwise_f16(x.numpy())
+    yr, accr = oracle.grouped_w8a8_f16(aq_r, as_r, w.numpy(), ws.numpy(), seg_r, row_index=ri,
+                                       bias=bias.numpy(), want_acc=True)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), yr.view(np.uint16))
+
+
 @pytest.mark.parametrize("T", [16, 256])
 def test_combine_bitexact(pkg, wl, cuda, T):
     E, k, H = wl.MOE["experts"], wl.MOE["top_k"], wl.MOE["hidden"]
