@@ -105,13 +105,17 @@ __device__ __forceinline__ uint32_t wave_max_uniform(uint32_t v) {
 // fma(r, yr, t) == fl(x/s) for every non-zero fp16 |x| <= amax (Markstein's
 // correction; checked exhaustively over all fp16 (x, amax) pairs by the CPU
 // test suite), so rint of it equals quant_one's rint(x / s).
+//
+// The rounding to an integer is one addition: for |v| < 2^22, adding
+// 1.5 * 2^23 rounds v to the nearest integer, ties to even (the default
+// rounding mode), and leaves it in the low bits of the sum as a two's
+// complement value.  No clamp is needed: |x| <= amax and s = fl(amax / 127)
+// (or eps / 127 > amax / 127) keep |v| <= 127 * (1 + 2^-23) < 127.5.
 __device__ __forceinline__ uint32_t quant_fast(float x, float s, float yr) {
     const float t = x * yr;
     const float r = __builtin_fmaf(-t, s, x);
-    float v = __builtin_fmaf(r, yr, t);
-    v = __builtin_rintf(v);
-    v = __builtin_fminf(__builtin_fmaxf(v, -FNI8_QMAX), FNI8_QMAX);
-    return (uint32_t)(int32_t)v & 0xffu;
+    const float v = __builtin_fmaf(r, yr, t);
+    return __builtin_bit_cast(uint32_t, v + 12582912.0f) & 0xffu;
 }
 
 // 8 fp16 (one 16-byte chunk) -> 8 int8; zeros unless `live` (finite scale, real row).

@@ -186,11 +186,13 @@ def moe_combine_f16(y_sorted, topi, topw, pos):
     return out
 
 
-def quant_identity_check(corrected: bool = True):
-    """(pairs, quotient mismatches for x != 0, rounded mismatches) of the
-    division-free quantization against fl(x / s) over every fp16 (x, amax) pair
-    with |x| <= amax (quant_identity.c); corrected=False drops the FMA
-    correction step."""
-    out = np.zeros(3, np.int64)
-    _load().oracle_quant_identity_check(0 if corrected else 1, _p(out))
+def quant_identity_check(corrected: bool = True, magic_slip: bool = False):
+    """(pairs, quotient mismatches for x != 0, rounded mismatches, int8 byte
+    mismatches) of the division-free quantization against fl(x / s) over every
+    fp16 (x, amax) pair with |x| <= amax (quant_identity.c).  corrected=False
+    drops the FMA correction step; magic_slip=True rounds with 2^23 instead of
+    1.5 * 2^23 (negative controls)."""
+    out = np.zeros(4, np.int64)
+    mode = 2 if magic_slip else (0 if corrected else 1)
+    _load().oracle_quant_identity_check(mode, _p(out))
     return tuple(int(v) for v in out)

@@ -14,10 +14,17 @@
  * x = +-0 the two may differ only in the sign of zero) and rint(v) with
  * rint(fl(x / s)).
  *
- * mode 0 checks that formula; mode 1 drops the correction (v = t), the
- * plausible shortcut, so that a test can show the check detects it.
+ * The kernels then round without rint, clamp or a float-to-int conversion:
+ * the int8 is the low byte of the bits of v + 1.5 * 2^23 (for |v| < 2^22 the
+ * addition rounds v to an integer, ties to even, and leaves it in the low bits
+ * in two's complement).  out[3] counts pairs where that byte differs from the
+ * oracle's int8, clamp(rint(fl(x / s)), -127, 127).
+ *
+ * mode 0 checks those formulas; mode 1 drops the correction (v = t), the
+ * plausible shortcut; mode 2 adds 2^23 instead of 1.5 * 2^23 (a plausible slip
+ * that breaks negative values) -- so that tests can show the check detects both.
  * out[0] = pairs checked, out[1] = quotient mismatches with x != 0,
- * out[2] = rounded-integer mismatches (any x).
+ * out[2] = rounded-integer mismatches (any x), out[3] = int8 byte mismatches.
  */
 #include <math.h>
 #include <stdint.h>
@@ -32,8 +39,9 @@ static float h2f_bits(uint16_t h) {
 }
 
 void oracle_quant_identity_check(int mode, int64_t* out) {
-    int64_t pairs = 0, bad_quot = 0, bad_int = 0;
-#pragma omp parallel for schedule(dynamic, 64) reduction(+ : pairs, bad_quot, bad_int)
+    int64_t pairs = 0, bad_quot = 0, bad_int = 0, bad_byte = 0;
+    const float magic = mode == 2 ? 8388608.0f : 12582912.0f;
+#pragma omp parallel for schedule(dynamic, 64) reduction(+ : pairs, bad_quot, bad_int, bad_byte)
     for (int a = 0; a < 0x7c00; a++) {
         const float amax = h2f_bits((uint16_t)a);
         const float num = amax > 1e-6f ? amax : 1e-6f;
@@ -45,14 +53,22 @@ void oracle_quant_identity_check(int mode, int64_t* out) {
                 const float v = x / s;
                 const float t = x * y;
                 const float r = fmaf(-t, s, x);
-                const float v2 = mode == 0 ? fmaf(r, y, t) : t;
+                const float v2 = mode == 1 ? t : fmaf(r, y, t);
                 pairs++;
                 if (x != 0.0f && memcmp(&v, &v2, sizeof v) != 0) bad_quot++;
                 if (rintf(v) != rintf(v2)) bad_int++;
+                float qf = rintf(v);
+                qf = qf > 127.0f ? 127.0f : (qf < -127.0f ? -127.0f : qf);
+                const int8_t q_ref = (int8_t)qf;
+                const float sum = v2 + magic;
+                uint32_t bits;
+                memcpy(&bits, &sum, sizeof bits);
+                if ((int8_t)(uint8_t)(bits & 0xffu) != q_ref) bad_byte++;
             }
         }
     }
     out[0] = pairs;
     out[1] = bad_quot;
     out[2] = bad_int;
+    out[3] = bad_byte;
 }

@@ -147,21 +147,30 @@ def test_quant_matches_numpy_fp32_restatement():
 
 
 def test_division_free_quant_identity_exhaustive():
-    """The GPU decode kernel quantizes with y = fl(1/s), t = fl(x*y),
-    v = fma(fma(-t, s, x), y, t) instead of fl(x/s).  Over every fp16 amax and
-    every fp16 x with |x| <= amax (about 10^9 pairs) the quotient is the same
-    bits for x != 0 and the rounded integer is always the same."""
-    pairs, bad_quot, bad_int = oracle.quant_identity_check()
+    """The GPU kernels quantize with y = fl(1/s), t = fl(x*y),
+    v = fma(fma(-t, s, x), y, t) instead of fl(x/s), and take the int8 as the low
+    byte of v + 1.5 * 2^23.  Over every fp16 amax and every fp16 x with
+    |x| <= amax (about 10^9 pairs) the quotient is the same bits for x != 0, the
+    rounded integer is always the same, and so is the int8."""
+    pairs, bad_quot, bad_int, bad_byte = oracle.quant_identity_check()
     assert pairs == 1007713280
-    assert bad_quot == 0 and bad_int == 0
+    assert bad_quot == 0 and bad_int == 0 and bad_byte == 0
 
 
 def test_division_free_quant_identity_check_detects_a_missing_correction():
     """Negative control: without the FMA correction (q = rint(fl(x * fl(1/s))))
     the same exhaustive sweep finds quotient and rounded-integer mismatches."""
-    pairs, bad_quot, bad_int = oracle.quant_identity_check(corrected=False)
+    pairs, bad_quot, bad_int, bad_byte = oracle.quant_identity_check(corrected=False)
     assert pairs == 1007713280
-    assert bad_quot > 0 and bad_int > 0
+    assert bad_quot > 0 and bad_int > 0 and bad_byte > 0
+
+
+def test_magic_rounding_check_detects_a_wrong_constant():
+    """Negative control: rounding with 2^23 instead of 1.5 * 2^23 (exact for
+    v >= 0, wrong for negative v) is caught by the int8 comparison."""
+    pairs, bad_quot, bad_int, bad_byte = oracle.quant_identity_check(magic_slip=True)
+    assert pairs == 1007713280
+    assert bad_quot == 0 and bad_int == 0 and bad_byte > 0
 
 
 # ---- int8 GEMM -------------------------------------------------------------
