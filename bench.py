@@ -17,6 +17,8 @@ Also reported (same JSON line):
                 5.0 POPS dense int8 MFMA peak
   moe           grouped expert GEMMs, 128 experts, top-8, T in {16, 256, 4096}
   stack         36 layers x 4 linears at decode M=32 then prefill M=2048
+  load          `.fni8` checkpoint load to HBM (whole file, one pipeline stage)
+                against a plain pinned host-to-device copy
   cpu_baseline  the reference's CPU path for the same linears (dequantize the
                 weight on every call, then F.linear in fp16;
                 fni8serve/layers/linear.py:28-31, :70-71), on a bounded sample
@@ -278,6 +280,71 @@ def stack_section(pkg, wl, pool, device):
     return out
 
 
+def load_section(pkg, pool, device, layers=2, reps=3):
+    """The `.fni8` container: `layers` layers of the pool (the four Qwen3-8B
+    linears, 192 MB a layer) written with a pipeline-stage shard index, then
+    loaded to the device from a warm page cache -- the whole file, and one
+    stage -- against a plain pinned host-to-device copy of the stage's size.
+    Every loaded byte is compared with the pool."""
+    import shutil
+    import tempfile
+
+    d = tempfile.mkdtemp(prefix="fni8_load_")
+    try:
+        path = os.path.join(d, "qwen3_8b_linears.fni8")
+        stages = []
+        with pkg.FQWriter(path) as w:
+            for li in range(layers):
+                stages.append([])
+                for lname, qt in pool[li].items():
+                    w.add(f"model.layers.{li}.{lname}", qt)
+                    stages[-1].append(f"model.layers.{li}.{lname}")
+            w.finalize(meta={"model": "Qwen3-8B linears", "layers": layers},
+                       shards={"pp_stages": stages})
+        with open(path, "rb") as f:  # warm the page cache
+            while f.read(64 << 20):
+                pass
+
+        def timed(shard):
+            best, got = None, None
+            for _ in range(reps):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                got = pkg.load_fni8_checkpoint(path, device=device, shard=shard)
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                best = dt if best is None else min(best, dt)
+            nbytes = sum(q.data.numel() * q.data.element_size() + q.scale.numel() * 4
+                         for q in got.values())
+            for name, q in got.items():
+                li, lname = int(name.split(".")[2]), name.split(".")[3]
+                ref = pool[li][lname]
+                if not (torch.equal(q.data, ref.data) and torch.equal(q.scale, ref.scale)):
+                    raise RuntimeError(f"loaded {name} differs from the saved weight")
+            del got
+            return nbytes, best
+
+        out = {"file_bytes": os.path.getsize(path), "page_cache": "warm"}
+        for key, shard in (("full", None), ("stage", f"pp:{layers - 1}")):
+            nb, t = timed(shard)
+            out[key] = {"bytes": nb, "ms": round(t * 1e3, 2), "GBps": round(nb / t / 1e9, 2)}
+        nb = out["stage"]["bytes"]
+        host = torch.empty(nb, dtype=torch.uint8, pin_memory=True)
+        dev = torch.empty(nb, dtype=torch.uint8, device=device)
+        dev.copy_(host)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            dev.copy_(host, non_blocking=True)
+        torch.cuda.synchronize()
+        t = (time.perf_counter() - t0) / reps
+        out["pinned_h2d_GBps"] = round(nb / t / 1e9, 2)
+        out["frac_of_pinned_h2d"] = round(out["stage"]["GBps"] / out["pinned_h2d_GBps"], 3)
+        return out
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+
+
 def cpu_baseline(wl, budget_s=40.0, per_linear_s=0.8):
     """The reference's CPU linear (dequantize W per call, then F.linear in fp16),
     on one layer's four linears at M in {1, 4, 16, 64}: each linear is called
@@ -327,7 +394,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--sections", default="roofline,prefill,moe,stack,cpu")
+    ap.add_argument("--sections", default="roofline,prefill,moe,stack,load,cpu")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the graph-replayed decode step (for counter runs of one section)")
     args = ap.parse_args()
@@ -414,6 +481,9 @@ def run_sections(result, sections, pkg, wl, pool, device):
     if "stack" in sections:
         result["stack"] = stack_section(pkg, wl, pool, device)
         log(f"stack: {result['stack']}")
+    if "load" in sections:
+        result["load"] = load_section(pkg, pool, device)
+        log(f"load: {result['load']}")
     if "cpu" in sections:
         result["cpu_baseline"] = cpu_baseline(wl)
         log(f"cpu_baseline: {result['cpu_baseline']}")

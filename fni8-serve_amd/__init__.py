@@ -7,6 +7,9 @@ callers):
     QTensor                       the quantized-weight container
     quantize_int8_rowwise(w)      load-time per-row weight quantization
     LinearW8A8, GatedMLP, SparseMoE, LMHead and the weight helpers
+    save_fni8, FQWriter, FQReader the `.fni8` checkpoint container
+    load_fni8_checkpoint, load_fni8_state_dict, checkpoint_info
+                                  the loader (fni8serve/loader.py:19-69)
 
 The arithmetic runs in libfni8amd.so (hand-written HIP kernels for gfx950,
 C ABI in include/fni8amd.h); this package is the host side.  The directory is
@@ -22,6 +25,8 @@ from .ops import (  # noqa: F401
     quantize_rowwise,
 )
 from .qtensor import QTensor  # noqa: F401
+from .container import FQReader, FQWriter, save_fni8  # noqa: F401
+from .loader import checkpoint_info, load_fni8_checkpoint, load_fni8_state_dict  # noqa: F401
 from .quant import quantize_int8_rowwise  # noqa: F401
 from .layers import (  # noqa: F401
     NF4_CODEBOOK,
@@ -41,5 +46,6 @@ __all__ = [
     "linear", "linear_with_intermediates", "quantize_rowwise", "gemm_w8a8", "gemm_w8a8_grouped",
     "moe_sort", "moe_combine", "QTensor", "quantize_int8_rowwise", "LinearW8A8", "GatedMLP",
     "Qwen3MLP", "SparseMoE", "LMHead", "NF4_CODEBOOK", "to_qtensor", "merge_qtensor",
-    "qkv_weight", "gate_up_weight",
+    "qkv_weight", "gate_up_weight", "save_fni8", "FQWriter", "FQReader", "load_fni8_checkpoint",
+    "load_fni8_state_dict", "checkpoint_info",
 ]
