@@ -17,6 +17,8 @@ Also reported (same JSON line):
                 5.0 POPS dense int8 MFMA peak
   moe           grouped expert GEMMs, 128 experts, top-8, T in {16, 256, 4096}
   stack         36 layers x 4 linears at decode M=32 then prefill M=2048
+  fusion        act_and_mul and RMSNorm kernels, alone and fused with the next
+                linear's quantization, and the chains they shorten (down, QKV)
   load          `.fni8` checkpoint load to HBM (whole file, one pipeline stage)
                 against a plain pinned host-to-device copy
   cpu_baseline  the reference's CPU path for the same linears (dequantize the
@@ -280,6 +282,70 @@ def stack_section(pkg, wl, pool, device):
     return out
 
 
+def time_burst(fn, reps):
+    """Mean time of `fn` over `reps` back-to-back calls, HIP events on the
+    launch stream; the burst is enqueued behind a GPU-side sleep so host launch
+    overhead does not open gaps between the kernels."""
+    fn()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.0e6 * reps + 2.0e7))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def fusion_section(pkg, wl, pool, device, ms=(1, 4, 16, 64, 2048, 4096)):
+    """The producers of the linears' inputs and their fused forms, at Qwen3-8B's
+    sizes (intermediate 12288 = down's K, hidden 4096 = QKV's K):
+      act_and_mul_quant   reads 4I bytes a row, writes I + 4 (HBM-bound)
+      rmsnorm_quant       with the residual add: reads 4K + the weight,
+                          writes 2K (new residual) + K + 4
+    each against the 8 TB/s peak; and the two chains they shorten, unfused vs
+    fused: act_and_mul -> linear(down) vs act_and_mul_quant -> gemm_w8a8(down),
+    rmsnorm -> linear(qkv) vs rmsnorm_quant -> gemm_w8a8(qkv)."""
+    I, H = 12288, 4096
+    g = torch.Generator(device=device).manual_seed(55)
+    w_norm = (torch.rand(H, device=device, generator=g) + 0.5).half()
+    down, qkv = pool[0]["down"], pool[0]["qkv"]
+    out = {}
+    for M in ms:
+        reps = 200 if M <= 64 else 20
+        h = (torch.randn(M, 2 * I, device=device, generator=g) * 2).half()
+        x = torch.randn(M, H, device=device, generator=g).half()
+        res = torch.randn(M, H, device=device, generator=g).half()
+        t_act = time_burst(lambda: pkg.act_and_mul(h, "silu"), reps)
+        t_actq = time_burst(lambda: pkg.act_and_mul_quant(h, "silu"), reps)
+        t_norm = time_burst(lambda: pkg.rmsnorm(x, w_norm, 1e-6, residual=res), reps)
+        t_normq = time_burst(lambda: pkg.rmsnorm_quant(x, w_norm, 1e-6, residual=res), reps)
+        b_actq = M * (4 * I + I + 4)
+        b_normq = M * (4 * H + 2 * H + H + 4) + 2 * H
+        t_down_u = time_burst(lambda: pkg.linear(pkg.act_and_mul(h, "silu"), down), reps)
+        t_down_f = time_burst(lambda: pkg.gemm_w8a8(*pkg.act_and_mul_quant(h, "silu"), down), reps)
+        t_qkv_u = time_burst(
+            lambda: pkg.linear(pkg.rmsnorm(x, w_norm, 1e-6, residual=res)[0], qkv), reps)
+        t_qkv_f = time_burst(
+            lambda: pkg.gemm_w8a8(*pkg.rmsnorm_quant(x, w_norm, 1e-6, residual=res)[:2], qkv), reps)
+        us = lambda t: round(t * 1e6, 2)  # noqa: E731
+        out[f"M{M}"] = {
+            "act_and_mul_us": us(t_act), "act_and_mul_quant_us": us(t_actq),
+            "act_and_mul_quant_GBps": round(b_actq / t_actq / 1e9, 1),
+            "act_and_mul_quant_pct_hbm": round(b_actq / t_actq / 1e9 / HBM_PEAK_GBS * 100, 1),
+            "rmsnorm_us": us(t_norm), "rmsnorm_quant_us": us(t_normq),
+            "rmsnorm_quant_GBps": round(b_normq / t_normq / 1e9, 1),
+            "rmsnorm_quant_pct_hbm": round(b_normq / t_normq / 1e9 / HBM_PEAK_GBS * 100, 1),
+            "down_chain_us": {"unfused": us(t_down_u), "fused": us(t_down_f),
+                              "speedup": round(t_down_u / t_down_f, 3)},
+            "qkv_chain_us": {"unfused": us(t_qkv_u), "fused": us(t_qkv_f),
+                             "speedup": round(t_qkv_u / t_qkv_f, 3)},
+        }
+        del h, x, res
+    return out
+
+
 def load_section(pkg, pool, device, layers=2, reps=3):
     """The `.fni8` container: `layers` layers of the pool (the four Qwen3-8B
     linears, 192 MB a layer) written with a pipeline-stage shard index, then
@@ -394,7 +460,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--sections", default="roofline,prefill,moe,stack,load,cpu")
+    ap.add_argument("--sections", default="roofline,prefill,moe,stack,fusion,load,cpu")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the graph-replayed decode step (for counter runs of one section)")
     args = ap.parse_args()
@@ -481,6 +547,9 @@ def run_sections(result, sections, pkg, wl, pool, device):
     if "stack" in sections:
         result["stack"] = stack_section(pkg, wl, pool, device)
         log(f"stack: {result['stack']}")
+    if "fusion" in sections:
+        result["fusion"] = fusion_section(pkg, wl, pool, device)
+        log(f"fusion: {result['fusion']}")
     if "load" in sections:
         result["load"] = load_section(pkg, pool, device)
         log(f"load: {result['load']}")

@@ -19,6 +19,8 @@ _ARG_ERRORS = (ERR_NULL, ERR_SHAPE, ERR_ALIGN, ERR_STRIDE)
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int64
+_C = ctypes.c_int
+_F = ctypes.c_float
 
 # name -> argument types; every entry point returns int
 SIGNATURES = {
@@ -28,6 +30,10 @@ SIGNATURES = {
     "fni8_moe_sort": [_P, _I, _I, _I, _P, _P, _P, _P],
     "fni8_gemm_w8a8_grouped": [_P, _P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _P, _P, _P],
     "fni8_moe_combine_f16": [_P, _I, _P, _P, _P, _I, _I, _P, _P],
+    "fni8_act_and_mul_f16": [_P, _I, _I, _I, _C, _P, _I, _P],
+    "fni8_act_and_mul_quant_f16": [_P, _I, _I, _I, _C, _P, _I, _P, _P],
+    "fni8_rmsnorm_f16": [_P, _I, _P, _I, _P, _F, _C, _I, _I, _P, _I, _P, _I, _P],
+    "fni8_rmsnorm_quant_f16": [_P, _I, _P, _I, _P, _F, _C, _I, _I, _P, _I, _P, _P, _I, _P],
 }
 STRING_FUNCS = ("fni8_strerror", "fni8_last_error", "fni8_version")
 

@@ -69,6 +69,24 @@ int check_gemm_shape(int64_t M, int64_t K, int64_t N) {
     return FNI8_OK;
 }
 
+int check_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr,
+                  const void* weight, float eps, int64_t M, int64_t K, int64_t ldo,
+                  const void* residual_out, int64_t ldro) {
+    REQUIRE(x && weight, FNI8_ERR_NULL, "x and weight are required");
+    REQUIRE(M >= 0 && M < kMaxDim && K > 0 && K < kMaxDim, FNI8_ERR_SHAPE,
+            "M=%lld K=%lld out of range", (long long)M, (long long)K);
+    REQUIRE(eps >= 0.0f && eps < __builtin_inff(), FNI8_ERR_SHAPE, "eps must be finite and >= 0");
+    REQUIRE(ldx >= K && ldo >= K, FNI8_ERR_STRIDE, "ldx=%lld or output stride %lld < K=%lld",
+            (long long)ldx, (long long)ldo, (long long)K);
+    REQUIRE(!residual || ldr >= K, FNI8_ERR_STRIDE, "ldr=%lld < K", (long long)ldr);
+    REQUIRE(!residual || !residual_out || ldro >= K, FNI8_ERR_STRIDE, "ldro=%lld < K",
+            (long long)ldro);
+    REQUIRE(aligned(x, 2) && aligned(residual, 2) && aligned(weight, 2) &&
+                aligned(residual_out, 2),
+            FNI8_ERR_ALIGN, "fp16 operands misaligned");
+    return FNI8_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -216,6 +234,75 @@ int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
     if (rc) return rc;
     return fni8h::launch_moe_combine((const uint16_t*)y_sorted, H, topi, (const uint16_t*)topw,
                                      pos, T, k, (uint16_t*)out, (hipStream_t)stream);
+}
+
+int fni8_act_and_mul_f16(const void* x, int64_t ldx, int64_t M, int64_t I, int act, void* out,
+                         int64_t ldo, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(x && out, FNI8_ERR_NULL, "x and out are required");
+    REQUIRE(M >= 0 && M < kMaxDim && I > 0 && I < kMaxDim / 2, FNI8_ERR_SHAPE,
+            "M=%lld I=%lld out of range", (long long)M, (long long)I);
+    REQUIRE(act == FNI8_ACT_SILU || act == FNI8_ACT_GELU_TANH, FNI8_ERR_SHAPE,
+            "unknown activation %d", act);
+    REQUIRE(ldx >= 2 * I && ldo >= I, FNI8_ERR_STRIDE, "ldx=%lld < 2I or ldo=%lld < I",
+            (long long)ldx, (long long)ldo);
+    REQUIRE(aligned(x, 2) && aligned(out, 2), FNI8_ERR_ALIGN, "x or out misaligned");
+    int rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_act_and_mul((const uint16_t*)x, ldx, M, I, act, (uint16_t*)out, ldo,
+                                     (hipStream_t)stream);
+}
+
+int fni8_act_and_mul_quant_f16(const void* x, int64_t ldx, int64_t M, int64_t I, int act,
+                               int8_t* xq, int64_t ldq, float* xs, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(x && xq && xs, FNI8_ERR_NULL, "x, xq and xs are required");
+    REQUIRE(M >= 0 && M < kMaxDim && I > 0 && I < kMaxDim / 2 && I % 4 == 0, FNI8_ERR_SHAPE,
+            "M=%lld I=%lld out of range (I a multiple of 4)", (long long)M, (long long)I);
+    REQUIRE(act == FNI8_ACT_SILU || act == FNI8_ACT_GELU_TANH, FNI8_ERR_SHAPE,
+            "unknown activation %d", act);
+    REQUIRE(ldx >= 2 * I && ldq >= I, FNI8_ERR_STRIDE, "ldx=%lld < 2I or ldq=%lld < I",
+            (long long)ldx, (long long)ldq);
+    REQUIRE(aligned(x, 2) && aligned(xs, 4), FNI8_ERR_ALIGN, "x or xs misaligned");
+    int rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_act_and_mul_quant((const uint16_t*)x, ldx, M, I, act, xq, ldq, xs,
+                                           (hipStream_t)stream);
+}
+
+int fni8_rmsnorm_f16(const void* x, int64_t ldx, const void* residual, int64_t ldr,
+                     const void* weight, float eps, int unit_offset, int64_t M, int64_t K,
+                     void* out, int64_t ldo, void* residual_out, int64_t ldro, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(out, FNI8_ERR_NULL, "out is required");
+    int rc = check_rmsnorm(x, ldx, residual, ldr, weight, eps, M, K, ldo, residual_out, ldro);
+    if (rc) return rc;
+    REQUIRE(aligned(out, 2), FNI8_ERR_ALIGN, "out misaligned");
+    rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_rmsnorm((const uint16_t*)x, ldx, (const uint16_t*)residual, ldr,
+                                 (const uint16_t*)weight, eps, unit_offset ? 1 : 0, M, K,
+                                 (uint16_t*)out, ldo,
+                                 residual ? (uint16_t*)residual_out : nullptr, ldro, nullptr, 0,
+                                 nullptr, (hipStream_t)stream);
+}
+
+int fni8_rmsnorm_quant_f16(const void* x, int64_t ldx, const void* residual, int64_t ldr,
+                           const void* weight, float eps, int unit_offset, int64_t M, int64_t K,
+                           int8_t* xq, int64_t ldq, float* xs, void* residual_out,
+                           int64_t ldro, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(xq && xs, FNI8_ERR_NULL, "xq and xs are required");
+    int rc = check_rmsnorm(x, ldx, residual, ldr, weight, eps, M, K, ldq, residual_out, ldro);
+    if (rc) return rc;
+    REQUIRE(K % 4 == 0, FNI8_ERR_SHAPE, "K=%lld is not a multiple of 4", (long long)K);
+    REQUIRE(aligned(xs, 4), FNI8_ERR_ALIGN, "xs misaligned");
+    rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_rmsnorm((const uint16_t*)x, ldx, (const uint16_t*)residual, ldr,
+                                 (const uint16_t*)weight, eps, unit_offset ? 1 : 0, M, K, nullptr,
+                                 0, residual ? (uint16_t*)residual_out : nullptr, ldro, xq, ldq,
+                                 xs, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -241,5 +241,15 @@ int launch_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E, int32_
 int launch_moe_combine(const uint16_t* yr, int64_t H, const int32_t* topi,
                        const uint16_t* topw, const int32_t* pos, int64_t T, int64_t k,
                        uint16_t* out, hipStream_t st);
+int launch_act_and_mul(const uint16_t* x, int64_t ldx, int64_t M, int64_t I, int act,
+                       uint16_t* out, int64_t ldo, hipStream_t st);
+int launch_act_and_mul_quant(const uint16_t* x, int64_t ldx, int64_t M, int64_t I, int act,
+                             int8_t* q, int64_t ldq, float* s, hipStream_t st);
+// RMSNorm; with q non-NULL the normed row is quantized into q/s instead of
+// being written to out.  res_out receives x + res (only with res).
+int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* res, int64_t ldr,
+                   const uint16_t* w, float eps, int unit, int64_t M, int64_t K, uint16_t* out,
+                   int64_t ldo, uint16_t* res_out, int64_t ldro, int8_t* q, int64_t ldq,
+                   float* s, hipStream_t st);
 void set_error_detail(const char* fmt, ...);
 }  // namespace fni8h

@@ -11,8 +11,9 @@ runs instead, with no host sync:
     quantize_rowwise  x quantized once per token (row-local, so every expert
                       reuses the same int8 row)
     grouped gate_up   one launch over all expert segments, rows gathered by token
-    act_and_mul       on the sorted rows
-    quantize_rowwise  per sorted row
+    act_and_mul_quant the activation and the per-row quantization of the sorted
+                      rows in one launch (bit-identical to act_and_mul then
+                      quantize_rowwise)
     grouped down      one launch
     moe_combine       weighted fp16 sum in ascending expert id (index_add_ order)
 
@@ -28,7 +29,8 @@ import torch.nn.functional as F
 
 from .. import ops
 from ..qtensor import QTensor
-from .mlp import GatedMLP, get_act_and_mul
+from .activation import fused_act, get_act_and_mul
+from .mlp import GatedMLP
 
 
 class SparseMoE(nn.Module):
@@ -114,8 +116,11 @@ class SparseMoE(nn.Module):
         xq, xs = ops.quantize_rowwise(xf)
         h = ops.gemm_w8a8_grouped(xq, xs, self.w_gate_up, self.s_gate_up, seg_off, R,
                                   row_index=row_token)
-        a = self.act_fn(h)
-        aq, as_ = ops.quantize_rowwise(a)
+        act = fused_act(self.act_fn)
+        if act is not None:
+            aq, as_ = ops.act_and_mul_quant(h, act)
+        else:
+            aq, as_ = ops.quantize_rowwise(self.act_fn(h))
         y = ops.gemm_w8a8_grouped(aq, as_, self.w_down, self.s_down, seg_off, R)
         return ops.moe_combine(y, topi, topw, pos)
 

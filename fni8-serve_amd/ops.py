@@ -221,3 +221,106 @@ def moe_combine(y_sorted: torch.Tensor, topi: torch.Tensor, topw: torch.Tensor,
             _lib.call("fni8_moe_combine_f16", _ptr(y_sorted), H, _ptr(topi), _ptr(topw), _ptr(pos),
                       T, k, _ptr(out), _stream(dev))
     return out
+
+
+_ACTS = {"silu": 0, "gelu_tanh": 1}
+
+
+def _act_code(act: str) -> int:
+    try:
+        return _ACTS[act]
+    except KeyError:
+        raise ValueError(f"unsupported fused activation {act!r} (silu, gelu_tanh)") from None
+
+
+def _merged_rows(x: torch.Tensor, name: str):
+    if x.dtype != _f16:
+        raise ValueError(f"{name} expects fp16 (got {x.dtype})")
+    if x.shape[-1] % 2:
+        raise ValueError(f"{name}: last dimension {x.shape[-1]} is not 2 * intermediate")
+    return _rows(x, x.shape[-1])
+
+
+def act_and_mul(x: torch.Tensor, act: str = "silu") -> torch.Tensor:
+    """fni8.act_and_mul(x, act): x fp16 [..., 2I] (gate | up) -> fp16 [..., I]
+    (fni8serve/layers/activation.py:24, :40)."""
+    dev = _require_cuda("act_and_mul", x)
+    code = _act_code(act)
+    x2, ldx = _merged_rows(x, "act_and_mul")
+    M, I = x2.shape[0], x2.shape[1] // 2
+    out = torch.empty((*x.shape[:-1], I), dtype=_f16, device=dev)
+    if M and I:
+        with torch.cuda.device(dev):
+            _lib.call("fni8_act_and_mul_f16", _ptr(x2), ldx, M, I, code, _ptr(out), I,
+                      _stream(dev))
+    return out
+
+
+def act_and_mul_quant(x: torch.Tensor, act: str = "silu"):
+    """act_and_mul with the next linear's per-token quantization fused in:
+    x fp16 [..., 2I] -> (xq int8 [M, I], xs fp32 [M]), bit-identical to
+    quantize_rowwise(act_and_mul(x, act))."""
+    dev = _require_cuda("act_and_mul_quant", x)
+    code = _act_code(act)
+    x2, ldx = _merged_rows(x, "act_and_mul_quant")
+    M, I = x2.shape[0], x2.shape[1] // 2
+    if I % 4:
+        raise ValueError(f"act_and_mul_quant: intermediate size {I} is not a multiple of 4")
+    xq = torch.empty((M, I), dtype=torch.int8, device=dev)
+    xs = torch.empty((M,), dtype=torch.float32, device=dev)
+    if M:
+        with torch.cuda.device(dev):
+            _lib.call("fni8_act_and_mul_quant_f16", _ptr(x2), ldx, M, I, code, _ptr(xq), I,
+                      _ptr(xs), _stream(dev))
+    return xq, xs
+
+
+def _norm_args(name, x, weight, residual):
+    dev = _require_cuda(name, x, weight, residual)
+    K = x.shape[-1]
+    if x.dtype != _f16 or weight.dtype != _f16:
+        raise ValueError(f"{name} expects fp16 x and weight (got {x.dtype}, {weight.dtype})")
+    if weight.numel() != K:
+        raise ValueError(f"{name}: weight has {weight.numel()} entries, x rows have {K}")
+    if residual is not None and (residual.dtype != _f16 or residual.shape != x.shape):
+        raise ValueError(f"{name}: residual must be fp16 with x's shape")
+    x2, ldx = _rows(x, K)
+    r2, ldr = (None, 0) if residual is None else _rows(residual, K)
+    return dev, K, x2, ldx, r2, ldr, weight.contiguous()
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+            residual: torch.Tensor | None = None, unit_offset: bool = False):
+    """fni8.rmsnorm(x, weight, eps, residual=, unit_offset=)
+    (fni8serve/layers/norm.py:51-52): the normed fp16 tensor, or
+    (normed, x + residual) when a residual is given."""
+    dev, K, x2, ldx, r2, ldr, w = _norm_args("rmsnorm", x, weight, residual)
+    M = x2.shape[0]
+    out = torch.empty(x.shape, dtype=_f16, device=dev)
+    new_res = None if residual is None else torch.empty(x.shape, dtype=_f16, device=dev)
+    if M:
+        with torch.cuda.device(dev):
+            _lib.call("fni8_rmsnorm_f16", _ptr(x2), ldx, _ptr(r2), ldr, _ptr(w),
+                      ctypes.c_float(eps), int(bool(unit_offset)), M, K, _ptr(out), K,
+                      _ptr(new_res), K, _stream(dev))
+    return out if residual is None else (out, new_res)
+
+
+def rmsnorm_quant(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                  residual: torch.Tensor | None = None, unit_offset: bool = False):
+    """rmsnorm with the next linear's per-token quantization fused in:
+    (xq int8 [M, K], xs fp32 [M]), or (xq, xs, x + residual) with a residual;
+    bit-identical to quantize_rowwise(rmsnorm(...))."""
+    dev, K, x2, ldx, r2, ldr, w = _norm_args("rmsnorm_quant", x, weight, residual)
+    if K % 4:
+        raise ValueError(f"rmsnorm_quant: K={K} is not a multiple of 4")
+    M = x2.shape[0]
+    xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    xs = torch.empty((M,), dtype=torch.float32, device=dev)
+    new_res = None if residual is None else torch.empty(x.shape, dtype=_f16, device=dev)
+    if M:
+        with torch.cuda.device(dev):
+            _lib.call("fni8_rmsnorm_quant_f16", _ptr(x2), ldx, _ptr(r2), ldr, _ptr(w),
+                      ctypes.c_float(eps), int(bool(unit_offset)), M, K, _ptr(xq), K, _ptr(xs),
+                      _ptr(new_res), K, _stream(dev))
+    return (xq, xs) if residual is None else (xq, xs, new_res)

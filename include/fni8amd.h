@@ -142,6 +142,75 @@ int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
                          const void* topw, const int32_t* pos, int64_t T, int64_t k,
                          void* out, void* stream);
 
+/* Gated activations of act_and_mul. */
+enum {
+    FNI8_ACT_SILU = 0,      /* "silu": g * sigmoid(g) */
+    FNI8_ACT_GELU_TANH = 1  /* "gelu_tanh": 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) */
+};
+
+/*
+ * Arithmetic of the activations (fp32, one rounding per operation): the gate
+ * is g * sigmoid(z), evaluated as g / (1 + exp(-z)) with z = g (silu) or
+ * z = 2 sqrt(2/pi) (g + 0.044715 g^3) (gelu_tanh, the same value as the tanh
+ * form); -z is clamped to [-86, 88] and exp is a Cody-Waite reduction with a
+ * degree-7 Taylor polynomial (error below 2 ulp).  out = fp16(gate * up).
+ */
+
+/*
+ * act_and_mul over a merged gate_up row: `fni8.act_and_mul(x, "silu" |
+ * "gelu_tanh")` (replaces fni8serve/layers/activation.py:24 and :40).
+ *   x    fp16 [M, 2I], row stride ldx elements: gate = x[:, :I], up = x[:, I:]
+ *   act  FNI8_ACT_SILU or FNI8_ACT_GELU_TANH
+ *   out  fp16 [M, I], row stride ldo elements (must not overlap x)
+ */
+int fni8_act_and_mul_f16(const void* x, int64_t ldx, int64_t M, int64_t I, int act, void* out,
+                         int64_t ldo, void* stream);
+
+/*
+ * act_and_mul with the per-token quantization of the down projection fused
+ * in: the int8 rows and scales are bit-identical to fni8_act_and_mul_f16
+ * followed by fni8_quantize_rowwise_f16, without the fp16 [M, I] round trip
+ * (replaces activation.py:24 and the quantize half of down_proj's
+ * fni8.linear, fni8serve/layers/mlp.py:39-40 -> linear.py:69).  Feed xq/xs to
+ * fni8_gemm_w8a8 or fni8_gemm_w8a8_grouped.
+ *   xq   int8 [M, I], row stride ldq bytes; xs fp32 [M]
+ * I must be a multiple of 4.
+ */
+int fni8_act_and_mul_quant_f16(const void* x, int64_t ldx, int64_t M, int64_t I, int act,
+                               int8_t* xq, int64_t ldq, float* xs, void* stream);
+
+/*
+ * RMSNorm: `fni8.rmsnorm(x, weight, eps, residual=, unit_offset=)` (replaces
+ * fni8serve/layers/norm.py:51-52; semantics of its eager form norm.py:37-58).
+ *   h = residual ? fp16(x + residual) : x
+ *   out = fp16((h * r) * w), r = 1 / sqrt(sum(h^2) / K + eps), w = weight or,
+ *         with unit_offset, 1 + weight (Gemma), all in fp32
+ * The sum of squares runs in a fixed order: 8-element chunks dealt round-robin
+ * to 256 accumulators, a butterfly within each group of 64, then
+ * (w0 + w1) + (w2 + w3).
+ *   x, residual (or NULL)  fp16 [M, K], row strides ldx, ldr elements
+ *   weight                 fp16 [K]
+ *   out                    fp16 [M, K], row stride ldo
+ *   residual_out           fp16 [M, K] (stride ldro) receiving h, or NULL;
+ *                          ignored without residual
+ * Outputs must not overlap inputs.
+ */
+int fni8_rmsnorm_f16(const void* x, int64_t ldx, const void* residual, int64_t ldr,
+                     const void* weight, float eps, int unit_offset, int64_t M, int64_t K,
+                     void* out, int64_t ldo, void* residual_out, int64_t ldro, void* stream);
+
+/*
+ * RMSNorm with the per-token quantization of the next linear (QKV, gate_up)
+ * fused in: xq/xs are bit-identical to fni8_rmsnorm_f16 followed by
+ * fni8_quantize_rowwise_f16 (replaces norm.py:51-52 and the quantize half of
+ * the following fni8.linear, linear.py:69).
+ *   xq int8 [M, K] (row stride ldq bytes), xs fp32 [M]; K a multiple of 4
+ */
+int fni8_rmsnorm_quant_f16(const void* x, int64_t ldx, const void* residual, int64_t ldr,
+                           const void* weight, float eps, int unit_offset, int64_t M, int64_t K,
+                           int8_t* xq, int64_t ldq, float* xs, void* residual_out,
+                           int64_t ldro, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,14 @@ parity pinning (how each function is checked, in tests/test_oracle.py):
   quant_identity_check -- not an oracle function: the exhaustive proof, over
       every fp16 (x, amax) pair, that the division-free quantization of the GPU
       decode kernel reproduces quant_rowwise_f16's division (quant_identity.c).
+  exp_cw / act_f32 / act_and_mul_f16 (act_norm_oracle.c; tests/test_oracle_act_norm.py)
+      -- float64 exp over a dense fp32 sweep (max error in ulp), the float64
+      closed forms of silu and the tanh gelu over every fp16 gate, known
+      answers, torch's eager fallback (F.silu(g) * u, F.gelu(g, "tanh") * u) and
+      torch's fp32 forms.
+  sumsq_fixed / rmsnorm_f16 -- math.fsum error bound, exact known answers,
+      float64 closed form, torch's eager RMSNorm (fni8serve/layers/norm.py:37-58)
+      and torch's fp16 residual add bit for bit, unit-offset identity.
 """
 from __future__ import annotations
 
@@ -60,10 +68,25 @@ def _load():
     lib.oracle_grouped_w8a8_f16.argtypes = [P, P, I, P, P, P, I, I, P, P, P, P]
     lib.oracle_moe_combine_f16.argtypes = [P, I, P, P, P, I, I, P]
     lib.oracle_quant_identity_check.argtypes = [ctypes.c_int, P]
+    F, C = ctypes.c_float, ctypes.c_int
+    lib.oracle_exp_cw.restype = F
+    lib.oracle_exp_cw.argtypes = [F]
+    lib.oracle_act_f32.restype = F
+    lib.oracle_act_f32.argtypes = [F, C]
+    lib.oracle_act_and_mul_f16.argtypes = [P, I, I, I, C, P, I]
+    lib.oracle_act_and_mul_quant_f16.argtypes = [P, I, I, I, C, P, P, I, P]
+    lib.oracle_exp_cw_n.argtypes = [P, P, I]
+    lib.oracle_act_f32_n.argtypes = [P, P, I, C]
+    lib.oracle_sumsq_fixed.restype = F
+    lib.oracle_sumsq_fixed.argtypes = [P, I]
+    lib.oracle_rmsnorm_f16.argtypes = [P, I, P, I, P, F, C, I, I, P, I, P, I, P]
+    lib.oracle_rmsnorm_quant_f16.argtypes = [P, I, P, I, P, F, C, I, I, P, P, I, P, P, I, P]
     for fn in ("oracle_f16_to_f32_n", "oracle_f32_to_f16_n", "oracle_quant_rowwise_f16",
                "oracle_gemm_i8", "oracle_dequant_f16", "oracle_linear_w8a8_f16",
                "oracle_grouped_w8a8_f16", "oracle_moe_combine_f16",
-               "oracle_quant_identity_check"):
+               "oracle_quant_identity_check", "oracle_act_and_mul_f16",
+               "oracle_act_and_mul_quant_f16", "oracle_rmsnorm_f16", "oracle_rmsnorm_quant_f16",
+               "oracle_exp_cw_n", "oracle_act_f32_n"):
         getattr(lib, fn).restype = None
     _lib = lib
     return lib
@@ -196,3 +219,81 @@ def quant_identity_check(corrected: bool = True, magic_slip: bool = False):
     mode = 2 if magic_slip else (0 if corrected else 1)
     _load().oracle_quant_identity_check(mode, _p(out))
     return tuple(int(v) for v in out)
+
+
+ACTS = {"silu": 0, "gelu_tanh": 1}
+
+
+def exp_cw(x) -> np.ndarray:
+    """The activations' fp32 exp (Cody-Waite reduction + degree-7 Taylor), x in [-86, 88]."""
+    x = _c(x, np.float32)
+    y = np.empty_like(x)
+    _load().oracle_exp_cw_n(_p(x), _p(y), x.size)
+    return y
+
+
+def act_f32(g, act: str) -> np.ndarray:
+    """The gate value act(g) in fp32 (silu or gelu_tanh), before the product with up."""
+    g = _c(g, np.float32)
+    y = np.empty_like(g)
+    _load().oracle_act_f32_n(_p(g), _p(y), g.size, ACTS[act])
+    return y
+
+
+def act_and_mul_f16(x: np.ndarray, act: str) -> np.ndarray:
+    """x fp16 [M, 2I] (gate | up) -> fp16 [M, I]."""
+    x = _c(x, np.float16)
+    M, I2 = x.shape
+    I = I2 // 2
+    out = np.empty((M, I), np.float16)
+    _load().oracle_act_and_mul_f16(_p(x), I2, M, I, ACTS[act], _p(out), I)
+    return out
+
+
+def act_and_mul_quant_f16(x: np.ndarray, act: str):
+    """x fp16 [M, 2I] -> (q int8 [M, I], s fp32 [M]): act_and_mul then quant_rowwise_f16."""
+    x = _c(x, np.float16)
+    M, I2 = x.shape
+    I = I2 // 2
+    tmp = np.empty((M, I), np.float16)
+    q = np.empty((M, I), np.int8)
+    s = np.empty((M,), np.float32)
+    _load().oracle_act_and_mul_quant_f16(_p(x), I2, M, I, ACTS[act], _p(tmp), _p(q), I, _p(s))
+    return q, s
+
+
+def sumsq_fixed(h: np.ndarray) -> np.float32:
+    """Sum of squares of one fp16 row in the RMSNorm kernels' fixed order."""
+    h = _c(h, np.float16).reshape(-1)
+    return np.float32(_load().oracle_sumsq_fixed(_p(h), h.size))
+
+
+def rmsnorm_f16(x, weight, eps, residual=None, unit_offset=False):
+    """x fp16 [M, K], weight fp16 [K] -> (out fp16 [M, K], x + residual fp16 or None)."""
+    x = _c(x, np.float16)
+    M, K = x.shape
+    w = _c(weight, np.float16)
+    r = None if residual is None else _c(residual, np.float16)
+    out = np.empty((M, K), np.float16)
+    ro = None if r is None else np.empty((M, K), np.float16)
+    tmp = np.empty((K,), np.float16)
+    _load().oracle_rmsnorm_f16(_p(x), K, _p(r), K, _p(w), float(np.float32(eps)),
+                               int(bool(unit_offset)), M, K, _p(out), K, _p(ro), K, _p(tmp))
+    return out, ro
+
+
+def rmsnorm_quant_f16(x, weight, eps, residual=None, unit_offset=False):
+    """-> (q int8 [M, K], s fp32 [M], x + residual fp16 or None): rmsnorm then quant."""
+    x = _c(x, np.float16)
+    M, K = x.shape
+    w = _c(weight, np.float16)
+    r = None if residual is None else _c(residual, np.float16)
+    normed = np.empty((M, K), np.float16)
+    q = np.empty((M, K), np.int8)
+    s = np.empty((M,), np.float32)
+    ro = None if r is None else np.empty((M, K), np.float16)
+    tmp = np.empty((K,), np.float16)
+    _load().oracle_rmsnorm_quant_f16(_p(x), K, _p(r), K, _p(w), float(np.float32(eps)),
+                                     int(bool(unit_offset)), M, K, _p(normed), _p(q), K, _p(s),
+                                     _p(ro), K, _p(tmp))
+    return q, s, ro

@@ -70,3 +70,31 @@ def test_argument_errors_return_before_any_launch(lib):
     assert rc == -2
     rc = lib.fni8_quantize_rowwise_f16(fake, -1, 64, 64, fake, 64, fake, None)
     assert rc == -2
+
+
+def test_act_and_norm_argument_errors(lib):
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call fails its checks
+    F = ctypes.c_float
+    # unknown activation code
+    assert lib.fni8_act_and_mul_f16(fake, 16, 1, 8, 7, fake, 8, None) == -2
+    assert b"activation" in lib.fni8_last_error()
+    # row stride shorter than gate | up
+    assert lib.fni8_act_and_mul_f16(fake, 15, 1, 8, 0, fake, 8, None) == -4
+    # the fused quantization needs I % 4 == 0 (the consuming GEMM's K rule)
+    assert lib.fni8_act_and_mul_quant_f16(fake, 20, 1, 10, 0, fake, 10, fake, None) == -2
+    assert lib.fni8_act_and_mul_quant_f16(None, 16, 1, 8, 0, fake, 8, fake, None) == -1
+    # rmsnorm: NaN / negative eps, short strides, missing weight, misaligned x
+    assert lib.fni8_rmsnorm_f16(fake, 8, None, 0, fake, F(float("nan")), 0, 1, 8, fake, 8,
+                                None, 0, None) == -2
+    assert lib.fni8_rmsnorm_f16(fake, 8, None, 0, fake, F(-1.0), 0, 1, 8, fake, 8, None, 0,
+                                None) == -2
+    assert lib.fni8_rmsnorm_f16(fake, 8, fake, 4, fake, F(1e-6), 0, 1, 8, fake, 8, fake, 8,
+                                None) == -4
+    assert lib.fni8_rmsnorm_f16(fake, 8, None, 0, None, F(1e-6), 0, 1, 8, fake, 8, None, 0,
+                                None) == -1
+    assert lib.fni8_rmsnorm_f16(ctypes.c_void_p(0x1001), 8, None, 0, fake, F(1e-6), 0, 1, 8,
+                                fake, 8, None, 0, None) == -3
+    assert lib.fni8_rmsnorm_quant_f16(fake, 10, None, 0, fake, F(1e-6), 0, 1, 10, fake, 10,
+                                      fake, None, 0, None) == -2
+    assert lib.fni8_rmsnorm_quant_f16(fake, 8, None, 0, fake, F(1e-6), 0, 1, 8, None, 8, fake,
+                                      None, 0, None) == -1

@@ -124,13 +124,39 @@ def test_gated_mlp_cpu_and_activations(pkg):
     y = mlp(torch.randn(3, 64).half())
     assert y.shape == (3, 64)
     from importlib import import_module
-    act = import_module("fni8serve_amd.layers.mlp")
+    act = import_module("fni8serve_amd.layers.activation")
     x = torch.randn(4, 32)
     g, u = x.chunk(2, -1)
     assert torch.allclose(act.SiluAndMul()(x), torch.nn.functional.silu(g) * u)
     assert isinstance(act.get_act_and_mul("gelu_pytorch_tanh"), act.GeluAndMul)
     with pytest.raises(ValueError):
         act.get_act_and_mul("relu")
+    assert act.fused_act(act.SiluAndMul()) == "silu"
+    assert act.fused_act(act.GeluAndMul("tanh")) == "gelu_tanh"
+    assert act.fused_act(act.GeluAndMul("none")) is None  # exact-erf gelu: eager only
+
+
+def test_rmsnorm_cpu_is_the_reference_eager_form(pkg):
+    """CPU tensors take norm.py:37-58's eager form: fp32 norm cast back, the
+    residual added in the input dtype and returned alongside."""
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(3, 64, generator=g).half()
+    r = torch.randn(3, 64, generator=g).half()
+    w = (torch.rand(64, generator=g) + 0.5).half()
+    n = pkg.RMSNorm(64, eps=1e-5, weight=w.clone())
+    xf = x.float()
+    want = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-5) * w.float()).half()
+    assert torch.equal(n(x), want)
+    out, new_r = n(x, r)
+    assert torch.equal(new_r, x + r)
+    hf = (x + r).float()
+    assert torch.equal(out, (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + 1e-5) * w.float()).half())
+    gem = pkg.RMSNorm(64, add_unit_offset=True)
+    assert torch.equal(gem.weight, torch.zeros(64, dtype=torch.float16))
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.rmsnorm(x, w)
+    with pytest.raises(ValueError, match="GPU"):
+        pkg.act_and_mul(torch.randn(2, 8).half())
 
 
 def _moe(pkg, E=4, H=64, I=32, k=2, **kw):
