@@ -16,6 +16,9 @@ Also reported (same JSON line):
   prefill       M in {512, 2048, 4096} on the four shapes: int8 TOPS against the
                 5.0 POPS dense int8 MFMA peak
   moe           grouped expert GEMMs, 128 experts, top-8, T in {16, 256, 4096}
+  moe_layer     the router kernel against torch's routing chain, and a whole
+                SparseMoE layer eager against the same layer replayed as one
+                HIP graph
   stack         36 layers x 4 linears at decode M=32 then prefill M=2048
   fusion        act_and_mul and RMSNorm kernels, alone and fused with the next
                 linear's quantization, and the chains they shorten (down, QKV)
@@ -265,6 +268,67 @@ def moe_section(pkg, wl, device, ts=(16, 256, 4096)):
     return out
 
 
+def moe_layer_section(pkg, wl, device, route_ts=(1, 16, 256, 4096), layer_ts=(1, 4, 16, 64)):
+    """A whole SparseMoE layer, Qwen3-30B-A3B-shaped (128 experts, top-8,
+    hidden 2048, expert intermediate 768, random int8 weights):
+      router       the torch chain the module ran before (softmax, topk,
+                   renormalise, cast: several launches) against the one-launch
+                   router kernel, on the same fp32 logits (device time)
+      layer        forward() eager against the same forward captured in one
+                   HIP graph and replayed: wall time per call, host included,
+                   and device time of back-to-back calls"""
+    E, k, H, I = (wl.MOE[n] for n in ("experts", "top_k", "hidden", "inter"))
+    g = torch.Generator(device=device).manual_seed(77)
+
+    def qt(n, kk):
+        q, s = pkg.quantize_int8_rowwise(torch.randn(n, kk, device=device, generator=g) * 0.02)
+        return pkg.QTensor(q, s.squeeze(-1), scheme="per_row_i8")
+
+    moe = pkg.SparseMoE(gate=(torch.randn(E, H, device=device, generator=g) * 0.05).half(),
+                        experts=[(qt(2 * I, H), qt(H, I)) for _ in range(E)], top_k=k)
+    out = {"router_us": {}, "layer_us": {}}
+    for T in route_ts:
+        logits = wl.router_logits(T, E, seed=T, device="cpu").to(device)
+        reps = 200 if T <= 256 else 50
+        t_torch = time_burst(lambda: wl.route(logits, k), reps)
+        t_kernel = time_burst(lambda: pkg.ops.moe_route(logits, k), reps)
+        out["router_us"][f"T{T}"] = {"torch_chain": round(t_torch * 1e6, 2),
+                                     "kernel": round(t_kernel * 1e6, 2),
+                                     "speedup": round(t_torch / t_kernel, 2)}
+    with torch.inference_mode():
+        for T in layer_ts:
+            x = (torch.randn(1, T, H, device=device, generator=g) * 0.5).half()
+            for _ in range(3):
+                moe(x)
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                moe(x)
+            torch.cuda.current_stream().wait_stream(s)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                moe(x)
+            reps = 100
+
+            def wall(fn):
+                fn()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for _ in range(reps):
+                    fn()
+                torch.cuda.synchronize()
+                return (time.perf_counter() - t0) / reps
+
+            w_eager, w_graph = wall(lambda: moe(x)), wall(graph.replay)
+            d_eager, d_graph = time_burst(lambda: moe(x), reps), time_burst(graph.replay, reps)
+            out["layer_us"][f"T{T}"] = {
+                "eager_wall": round(w_eager * 1e6, 1), "graph_wall": round(w_graph * 1e6, 1),
+                "wall_speedup": round(w_eager / w_graph, 2),
+                "eager_device": round(d_eager * 1e6, 1), "graph_device": round(d_graph * 1e6, 1)}
+            del graph
+    return out
+
+
 def stack_section(pkg, wl, pool, device):
     out = {}
     for M in (32, 2048):
@@ -460,7 +524,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--sections", default="roofline,prefill,moe,stack,fusion,load,cpu")
+    ap.add_argument("--sections", default="roofline,prefill,moe,moe_layer,stack,fusion,load,cpu")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the graph-replayed decode step (for counter runs of one section)")
     args = ap.parse_args()
@@ -544,6 +608,9 @@ def run_sections(result, sections, pkg, wl, pool, device):
     if "moe" in sections:
         result["moe"] = moe_section(pkg, wl, device)
         log(f"moe: {result['moe']}")
+    if "moe_layer" in sections:
+        result["moe_layer"] = moe_layer_section(pkg, wl, device)
+        log(f"moe_layer: {result['moe_layer']}")
     if "stack" in sections:
         result["stack"] = stack_section(pkg, wl, pool, device)
         log(f"stack: {result['stack']}")

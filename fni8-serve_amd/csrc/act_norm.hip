@@ -27,33 +27,12 @@ constexpr int kThreads = 256;
 
 // ---- activations ------------------------------------------------------------
 
-// exp(x) for x in [-86, 88].  Cody-Waite reduction x = k ln2 + r, |r| <= ln2/2,
-// with ln2 split into a 15-bit head (k * head is exact for |k| <= 127) and a
-// tail; exp(r) by its degree-7 Taylor polynomial in Horner form (truncation
-// below 0.14 ulp on the interval); 2^k applied through the exponent field
-// (k + 127 stays in [3, 254], so the result is a normal number).
-__device__ __forceinline__ float exp_cw(float x) {
-    const float k = __builtin_rintf(x * 0x1.715476p+0f);
-    float r = __builtin_fmaf(-k, 0x1.62e4p-1f, x);
-    r = __builtin_fmaf(-k, 0x1.7f7d1cp-20f, r);
-    float p = 0x1.a01a02p-13f;              // 1/7!
-    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);  // 1/6!
-    p = __builtin_fmaf(p, r, 0x1.111112p-7f);   // 1/5!
-    p = __builtin_fmaf(p, r, 0x1.555556p-5f);   // 1/4!
-    p = __builtin_fmaf(p, r, 0x1.555556p-3f);   // 1/3!
-    p = __builtin_fmaf(p, r, 0.5f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    p = __builtin_fmaf(p, r, 1.0f);
-    const float two_k = __builtin_bit_cast(float, (uint32_t)((int)k + 127) << 23);
-    return p * two_k;
-}
-
 // g / (1 + exp(t)), t clamped to [-86, 88] (a NaN t is taken as -86; a NaN g
 // still gives NaN).
 __device__ __forceinline__ float gated(float g, float t) {
     t = t >= -86.0f ? t : -86.0f;
     t = t <= 88.0f ? t : 88.0f;
-    return g / (1.0f + exp_cw(t));
+    return g / (1.0f + fni8::exp_cw(t));
 }
 
 // silu(g) = g * sigmoid(g).  gelu, tanh form: 0.5 g (1 + tanh(y)) with

@@ -236,6 +236,33 @@ int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
                                      pos, T, k, (uint16_t*)out, (hipStream_t)stream);
 }
 
+int fni8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ldl, int scoring,
+                   const float* bias, int64_t groups, int64_t topk_group, int64_t k, int renorm,
+                   float scale, void* topw, int32_t* topi, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(logits && topw && topi, FNI8_ERR_NULL, "logits, topw and topi are required");
+    REQUIRE(T >= 0 && T < kMaxDim && E >= 1 && E <= 1024, FNI8_ERR_SHAPE,
+            "T=%lld E=%lld out of range (E <= 1024)", (long long)T, (long long)E);
+    REQUIRE(k >= 1 && k <= 32 && k <= E, FNI8_ERR_SHAPE, "k=%lld out of range (1..min(32, E))",
+            (long long)k);
+    REQUIRE(scoring == FNI8_SCORE_SOFTMAX || scoring == FNI8_SCORE_SIGMOID, FNI8_ERR_SHAPE,
+            "unknown scoring function %d", scoring);
+    REQUIRE(groups == 0 || (groups >= 1 && groups <= 64 && E % groups == 0 && topk_group >= 1 &&
+                            topk_group <= groups),
+            FNI8_ERR_SHAPE, "groups=%lld topk_group=%lld invalid for E=%lld", (long long)groups,
+            (long long)topk_group, (long long)E);
+    REQUIRE(scale == scale && scale > -__builtin_inff() && scale < __builtin_inff(),
+            FNI8_ERR_SHAPE, "scale must be finite");
+    REQUIRE(ldl >= E, FNI8_ERR_STRIDE, "ldl=%lld < E=%lld", (long long)ldl, (long long)E);
+    REQUIRE(aligned(logits, 4) && aligned(bias, 4) && aligned(topw, 2) && aligned(topi, 4),
+            FNI8_ERR_ALIGN, "router operands misaligned");
+    int rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_moe_route(logits, ldl, T, E, scoring, bias, groups, topk_group, k,
+                                   renorm ? 1 : 0, scale, (uint16_t*)topw, topi,
+                                   (hipStream_t)stream);
+}
+
 int fni8_act_and_mul_f16(const void* x, int64_t ldx, int64_t M, int64_t I, int act, void* out,
                          int64_t ldo, void* stream) {
     fni8h::g_detail[0] = 0;

@@ -65,6 +65,27 @@ __device__ __forceinline__ uint16_t dequant_one(int32_t acc, float as, float ws,
     return f2h(v);
 }
 
+// exp(x) for x in [-86, 88].  Cody-Waite reduction x = k ln2 + r, |r| <= ln2/2,
+// with ln2 split into a 15-bit head (k * head is exact for |k| <= 127) and a
+// tail; exp(r) by its degree-7 Taylor polynomial in Horner form (truncation
+// below 0.14 ulp on the interval); 2^k applied through the exponent field
+// (k + 127 stays in [3, 254], so the result is a normal number).
+__device__ __forceinline__ float exp_cw(float x) {
+    const float k = __builtin_rintf(x * 0x1.715476p+0f);
+    float r = __builtin_fmaf(-k, 0x1.62e4p-1f, x);
+    r = __builtin_fmaf(-k, 0x1.7f7d1cp-20f, r);
+    float p = 0x1.a01a02p-13f;              // 1/7!
+    p = __builtin_fmaf(p, r, 0x1.6c16c2p-10f);  // 1/6!
+    p = __builtin_fmaf(p, r, 0x1.111112p-7f);   // 1/5!
+    p = __builtin_fmaf(p, r, 0x1.555556p-5f);   // 1/4!
+    p = __builtin_fmaf(p, r, 0x1.555556p-3f);   // 1/3!
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float two_k = __builtin_bit_cast(float, (uint32_t)((int)k + 127) << 23);
+    return p * two_k;
+}
+
 // ---- wave reductions and the division-free quantization --------------------
 // DPP lane permutations (gfx9 encodings).
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
@@ -251,5 +272,8 @@ int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* res, int64_t 
                    const uint16_t* w, float eps, int unit, int64_t M, int64_t K, uint16_t* out,
                    int64_t ldo, uint16_t* res_out, int64_t ldro, int8_t* q, int64_t ldq,
                    float* s, hipStream_t st);
+int launch_moe_route(const float* logits, int64_t ldl, int64_t T, int64_t E, int scoring,
+                     const float* bias, int64_t groups, int64_t topk_group, int64_t k, int renorm,
+                     float scale, uint16_t* topw, int32_t* topi, hipStream_t st);
 void set_error_detail(const char* fmt, ...);
 }  // namespace fni8h

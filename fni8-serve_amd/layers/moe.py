@@ -4,9 +4,13 @@ Same constructor and routing as fni8serve/models/moe.py:25-113 (softmax or
 sigmoid scoring, optional group-limited top-k, renormalisation, routed
 scaling, optional shared expert).  The reference then loops over experts in
 Python, with two host syncs per expert (moe.py:218-224); its docstring names
-the grouped GEMM as the intended kernel (moe.py:9-11).  On the GPU this module
-runs instead, with no host sync:
+the grouped GEMM as the intended kernel (moe.py:9-11), and its graph runner
+declines MoE layers for that reason (engine/cuda_graph.py:190-191).  On the
+GPU this module runs instead, with no host sync, so a whole MoE layer can be
+captured in a HIP graph:
 
+    router GEMM       fp32 logits (torch)
+    moe_route         scoring, group mask, top-k, weights in one launch
     moe_sort          stable counting sort of (token, slot) by expert
     quantize_rowwise  x quantized once per token (row-local, so every expert
                       reuses the same int8 row)
@@ -80,9 +84,26 @@ class SparseMoE(nn.Module):
         self.shared_gate = (nn.Parameter(shared_expert_gate)
                             if shared_expert_gate is not None else None)
 
+    def _gate_f32(self) -> torch.Tensor:
+        """The router weight in fp32 (moe.py:64 converts it on every call); the
+        copy is kept while the parameter's storage and version are unchanged."""
+        w = self.gate
+        key = (w.data_ptr(), w._version, w.device)
+        if getattr(self, "_gate_key", None) != key:
+            self._gate_cache = w.detach().float()
+            self._gate_key = key
+        return self._gate_cache
+
     def route(self, xf: torch.Tensor):
-        """Router (moe.py:184-214): returns (topw in x.dtype [T, k], topi [T, k])."""
-        router_logits = F.linear(xf.float(), self.gate.float())
+        """Router (moe.py:62-91): returns (topw in x.dtype [T, k], topi [T, k]).
+        On the GPU the scoring, group mask, top-k and weights are one launch
+        (`ops.moe_route`) after the fp32 router GEMM; on the CPU the
+        reference's torch chain runs as written."""
+        router_logits = F.linear(xf.float(), self._gate_f32())
+        if xf.is_cuda:
+            return ops.moe_route(router_logits, self.top_k, self.scoring_func, self.e_score_bias,
+                                 self.num_expert_groups, self.topk_group, self.norm_topk_prob,
+                                 self.routed_scaling_factor)
         if self.scoring_func == "sigmoid":
             scores = torch.sigmoid(router_logits)
             sel = scores + self.e_score_bias if self.e_score_bias is not None else scores

@@ -324,3 +324,36 @@ def rmsnorm_quant(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
                       ctypes.c_float(eps), int(bool(unit_offset)), M, K, _ptr(xq), K, _ptr(xs),
                       _ptr(new_res), K, _stream(dev))
     return (xq, xs) if residual is None else (xq, xs, new_res)
+
+
+_SCORES = {"softmax": 0, "sigmoid": 1}
+
+
+def moe_route(logits: torch.Tensor, top_k: int, scoring: str = "softmax",
+              bias: torch.Tensor | None = None, num_groups: int | None = None,
+              topk_group: int | None = None, renorm: bool = True, scale: float = 1.0):
+    """Router of SparseMoE (fni8serve/models/moe.py:62-91) in one launch:
+    logits fp32 [T, E] -> (topw fp16 [T, k], topi int32 [T, k]), best first."""
+    dev = _require_cuda("moe_route", logits, bias)
+    if logits.dtype != torch.float32 or logits.dim() != 2:
+        raise ValueError("moe_route expects fp32 logits [T, E]")
+    if scoring not in _SCORES:
+        raise ValueError(f"unsupported scoring function {scoring!r} (softmax, sigmoid)")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    T, E = logits.shape
+    if bias is not None:
+        if bias.numel() != E:
+            raise ValueError(f"bias has {bias.numel()} entries, expected {E}")
+        bias = bias.reshape(-1).float().contiguous()
+    groups = 0 if num_groups is None or topk_group is None else int(num_groups)
+    tg = 0 if groups == 0 else int(topk_group)
+    topw = torch.empty((T, top_k), dtype=_f16, device=dev)
+    topi = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+    if T:
+        ldl = logits.stride(0) if T > 1 else E
+        with torch.cuda.device(dev):
+            _lib.call("fni8_moe_route", _ptr(logits), T, E, ldl, _SCORES[scoring], _ptr(bias),
+                      groups, tg, top_k, int(bool(renorm)), ctypes.c_float(scale), _ptr(topw),
+                      _ptr(topi), _stream(dev))
+    return topw, topi

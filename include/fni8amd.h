@@ -142,6 +142,38 @@ int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
                          const void* topw, const int32_t* pos, int64_t T, int64_t k,
                          void* out, void* stream);
 
+/* Router scoring functions of fni8_moe_route. */
+enum {
+    FNI8_SCORE_SOFTMAX = 0, /* softmax over all experts (Qwen, Hunyuan, MiniMax) */
+    FNI8_SCORE_SIGMOID = 1  /* sigmoid per expert (GLM, DeepSeek, LFM2) */
+};
+
+/*
+ * MoE router, one launch: scores, optional selection bias, optional
+ * group-limited mask, top-k, weights (replaces the routing of
+ * SparseMoE.forward, fni8serve/models/moe.py:62-97, and the torch.topk /
+ * gather / renormalisation launches it makes; no host synchronisation, so an
+ * MoE layer can be captured in a HIP graph).
+ *   logits      fp32 [T, E] router logits, row stride ldl (>= E); E <= 1024
+ *   scoring     FNI8_SCORE_SOFTMAX or FNI8_SCORE_SIGMOID
+ *   bias        fp32 [E] added to the scores for selection only, or NULL
+ *   groups      0, or the number of expert groups (<= 64, dividing E): only
+ *               experts of the topk_group best groups (group score = max of
+ *               the biased scores) are selectable
+ *   k           experts per token, 1 <= k <= min(32, E)
+ *   renorm      non-zero: weights divided by max(their sum, 1e-9)
+ *   scale       routed scaling factor applied last
+ *   topw        fp16 [T, k]: softmax -> the selected scores; sigmoid -> the
+ *               selected unbiased scores; topi int32 [T, k], best first
+ * Arithmetic is fp32 with one rounding per operation; softmax sums in a
+ * fixed order, exp is the activations' Cody-Waite exp.  Top-k order: larger
+ * score first, NaN above +inf, ties to the lower expert index, -0 as +0 (the
+ * order torch.topk gives).
+ */
+int fni8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ldl, int scoring,
+                   const float* bias, int64_t groups, int64_t topk_group, int64_t k, int renorm,
+                   float scale, void* topw, int32_t* topi, void* stream);
+
 /* Gated activations of act_and_mul. */
 enum {
     FNI8_ACT_SILU = 0,      /* "silu": g * sigmoid(g) */

@@ -26,6 +26,10 @@ parity pinning (how each function is checked, in tests/test_oracle.py):
       closed forms of silu and the tanh gelu over every fp16 gate, known
       answers, torch's eager fallback (F.silu(g) * u, F.gelu(g, "tanh") * u) and
       torch's fp32 forms.
+  moe_route (route_oracle.c) -- float64 softmax / sigmoid, brute-force top-k by
+      sorting (value desc, index asc), the reference's torch routing
+      (fni8serve/models/moe.py:62-97) on the CPU: same experts, weights within
+      1 fp16 ulp; known answers (ties, groups, NaN rows, renormalisation).
   sumsq_fixed / rmsnorm_f16 -- math.fsum error bound, exact known answers,
       float64 closed form, torch's eager RMSNorm (fni8serve/layers/norm.py:37-58)
       and torch's fp16 residual add bit for bit, unit-offset identity.
@@ -77,6 +81,7 @@ def _load():
     lib.oracle_act_and_mul_quant_f16.argtypes = [P, I, I, I, C, P, P, I, P]
     lib.oracle_exp_cw_n.argtypes = [P, P, I]
     lib.oracle_act_f32_n.argtypes = [P, P, I, C]
+    lib.oracle_moe_route.argtypes = [P, I, I, I, C, P, I, I, I, C, F, P, P]
     lib.oracle_sumsq_fixed.restype = F
     lib.oracle_sumsq_fixed.argtypes = [P, I]
     lib.oracle_rmsnorm_f16.argtypes = [P, I, P, I, P, F, C, I, I, P, I, P, I, P]
@@ -86,7 +91,7 @@ def _load():
                "oracle_grouped_w8a8_f16", "oracle_moe_combine_f16",
                "oracle_quant_identity_check", "oracle_act_and_mul_f16",
                "oracle_act_and_mul_quant_f16", "oracle_rmsnorm_f16", "oracle_rmsnorm_quant_f16",
-               "oracle_exp_cw_n", "oracle_act_f32_n"):
+               "oracle_exp_cw_n", "oracle_act_f32_n", "oracle_moe_route"):
         getattr(lib, fn).restype = None
     _lib = lib
     return lib
@@ -297,3 +302,19 @@ def rmsnorm_quant_f16(x, weight, eps, residual=None, unit_offset=False):
                                      int(bool(unit_offset)), M, K, _p(normed), _p(q), K, _p(s),
                                      _p(ro), K, _p(tmp))
     return q, s, ro
+
+
+SCORES = {"softmax": 0, "sigmoid": 1}
+
+
+def moe_route(logits, k, scoring="softmax", bias=None, groups=0, topk_group=0, renorm=True,
+              scale=1.0):
+    """logits fp32 [T, E] -> (topw fp16 [T, k], topi int32 [T, k])."""
+    lg = _c(logits, np.float32)
+    T, E = lg.shape
+    b = None if bias is None else _c(bias, np.float32)
+    topw = np.empty((T, k), np.float16)
+    topi = np.empty((T, k), np.int32)
+    _load().oracle_moe_route(_p(lg), T, E, E, SCORES[scoring], _p(b), groups, topk_group, k,
+                             int(bool(renorm)), float(np.float32(scale)), _p(topw), _p(topi))
+    return topw, topi

@@ -98,3 +98,22 @@ def test_act_and_norm_argument_errors(lib):
                                       fake, None, 0, None) == -2
     assert lib.fni8_rmsnorm_quant_f16(fake, 8, None, 0, fake, F(1e-6), 0, 1, 8, None, 8, fake,
                                       None, 0, None) == -1
+
+
+def test_moe_route_argument_errors(lib):
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call fails its checks
+    F = ctypes.c_float
+    # E above 1024, k above 32 or E, unknown scoring
+    assert lib.fni8_moe_route(fake, 1, 2048, 2048, 0, None, 0, 0, 8, 1, F(1.0), fake, fake, None) == -2
+    assert lib.fni8_moe_route(fake, 1, 128, 128, 0, None, 0, 0, 33, 1, F(1.0), fake, fake, None) == -2
+    assert lib.fni8_moe_route(fake, 1, 4, 4, 0, None, 0, 0, 5, 1, F(1.0), fake, fake, None) == -2
+    assert lib.fni8_moe_route(fake, 1, 128, 128, 2, None, 0, 0, 8, 1, F(1.0), fake, fake, None) == -2
+    # groups must divide E, be <= 64, and topk_group within [1, groups]
+    assert lib.fni8_moe_route(fake, 1, 100, 100, 1, None, 8, 4, 8, 1, F(1.0), fake, fake, None) == -2
+    assert lib.fni8_moe_route(fake, 1, 256, 256, 1, None, 128, 4, 8, 1, F(1.0), fake, fake, None) == -2
+    assert lib.fni8_moe_route(fake, 1, 256, 256, 1, None, 8, 9, 8, 1, F(1.0), fake, fake, None) == -2
+    # non-finite scale, short stride, NULL output
+    assert lib.fni8_moe_route(fake, 1, 128, 128, 0, None, 0, 0, 8, 1, F(float("inf")), fake, fake,
+                              None) == -2
+    assert lib.fni8_moe_route(fake, 2, 128, 100, 0, None, 0, 0, 8, 1, F(1.0), fake, fake, None) == -4
+    assert lib.fni8_moe_route(fake, 1, 128, 128, 0, None, 0, 0, 8, 1, F(1.0), None, fake, None) == -1

@@ -215,3 +215,21 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_moe_router_weight_cache_follows_the_parameter(pkg):
+    """The fp32 router weight is cached; an in-place update of the parameter
+    (its version changes) or a new tensor is picked up on the next call."""
+    moe = _moe(pkg)
+    xf = torch.randn(5, 64)
+    w1, i1 = moe.route(xf)
+    assert torch.equal(moe._gate_f32(), moe.gate.detach().float())
+    with torch.no_grad():
+        moe.gate.mul_(-1.0)
+    w2, i2 = moe.route(xf)
+    assert torch.equal(moe._gate_f32(), moe.gate.detach().float())
+    assert not torch.equal(i1, i2)
+    moe.gate = torch.nn.Parameter(torch.zeros_like(moe.gate))
+    w3, i3 = moe.route(xf)
+    assert torch.equal(moe._gate_f32(), torch.zeros_like(moe.gate, dtype=torch.float32))
+    assert (w3 == 1.0 / moe.top_k).all()  # uniform scores, renormalised
