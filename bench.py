@@ -15,6 +15,8 @@ Also reported (same JSON line):
                 events on the launch stream, against the 8 TB/s HBM peak
   prefill       M in {512, 2048, 4096} on the four shapes: int8 TOPS against the
                 5.0 POPS dense int8 MFMA peak
+  w4a8          the same four shapes with per_group_i4 int4 weights (group 128):
+                decode GB/s against 8 TB/s, prefill TOPS against 5.0 POPS
   moe           grouped expert GEMMs, 128 experts, top-8, T in {16, 256, 4096}
   moe_layer     the router kernel against torch's routing chain, and a whole
                 SparseMoE layer eager against the same layer replayed as one
@@ -265,6 +267,54 @@ def moe_section(pkg, wl, device, ts=(16, 256, 4096)):
                         "pct_hbm_peak": round(b / t / 1e9 / HBM_PEAK_GBS * 100, 1),
                         "TOPS": round(ops / t / 1e12, 2),
                         "pct_mfma_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS * 100, 2)}
+    return out
+
+
+def w4a8_section(pkg, wl, device, layers=36, G=128, decode_ms=(1, 4, 16, 64),
+                 prefill_ms=(512, 2048, 4096)):
+    """W4A8 linears (per_group_i4 int4 weights, group size 128, the converter's
+    default) at Qwen3-8B's four shapes over a `layers`-deep pool of distinct
+    weights (3.5 GB: streamed from HBM).  Decode: algorithmic bytes (packed
+    weights + group scales + x + y) per second against 8 TB/s; prefill: int8
+    TOPS against 5.0 POPS."""
+    g = torch.Generator(device=device).manual_seed(88)
+    pool = []
+    for _ in range(layers):
+        entry = {}
+        for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
+            packed = torch.randint(0, 256, (N, K // 2), device=device, generator=g,
+                                   dtype=torch.int32).to(torch.uint8)
+            scale = torch.rand(N, K // G, device=device, generator=g) * 0.02 + 1e-3
+            entry[name] = pkg.QTensor(packed, scale, scheme="per_group_i4", group_size=G,
+                                      codebook="int4")
+        pool.append(entry)
+
+    def nbytes(M, N, K):
+        return N * K // 2 + 4 * N * (K // G) + 2 * M * K + 2 * M * N
+
+    out = {"decode": {}, "prefill": {}}
+    for M in decode_ms + prefill_ms:
+        xs = {K: wl.activations(M, K, seed=M + K, device="cpu").to(device) for K in (4096, 12288)}
+        per, tot_b, tot_t, ops = {}, 0, 0.0, 0
+        for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
+            x = xs[K]
+            reps = 1 if M > 64 else 2
+
+            def fn(name=name, x=x):
+                for layer in pool:
+                    pkg.linear(x, layer[name])
+            t = time_burst(fn, reps) / len(pool)
+            b = nbytes(M, N, K)
+            per[name] = {"us": round(t * 1e6, 2), "GBps": round(b / t / 1e9, 1),
+                         "TOPS": round(2 * M * N * K / t / 1e12, 1)}
+            tot_b += b
+            tot_t += t
+            ops += 2 * M * N * K
+        key = "decode" if M in decode_ms else "prefill"
+        out[key][f"M{M}"] = {"per_linear": per, "GBps": round(tot_b / tot_t / 1e9, 1),
+                             "pct_hbm_peak": round(tot_b / tot_t / 1e9 / HBM_PEAK_GBS * 100, 1),
+                             "TOPS": round(ops / tot_t / 1e12, 1),
+                             "pct_mfma_peak": round(ops / tot_t / 1e12 / INT8_PEAK_TOPS * 100, 1)}
     return out
 
 
@@ -524,7 +574,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--sections", default="roofline,prefill,moe,moe_layer,stack,fusion,load,cpu")
+    ap.add_argument("--sections", default="roofline,prefill,w4a8,moe,moe_layer,stack,fusion,load,cpu")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the graph-replayed decode step (for counter runs of one section)")
     args = ap.parse_args()
@@ -608,6 +658,9 @@ def run_sections(result, sections, pkg, wl, pool, device):
     if "moe" in sections:
         result["moe"] = moe_section(pkg, wl, device)
         log(f"moe: {result['moe']}")
+    if "w4a8" in sections:
+        result["w4a8"] = w4a8_section(pkg, wl, device)
+        log(f"w4a8: {result['w4a8']}")
     if "moe_layer" in sections:
         result["moe_layer"] = moe_layer_section(pkg, wl, device)
         log(f"moe_layer: {result['moe_layer']}")

@@ -3,7 +3,8 @@
 Drop-in pieces for the reference's seam (fni8serve/layers/linear.py and its
 callers):
 
-    linear(x, qt, bias=None)      the `fni8.linear` call (linear.py:69)
+    linear(x, qt, bias=None)      the `fni8.linear` call (linear.py:69), W8A8
+                                  (per_row_i8) and W4A8 (per_group_i4 int4)
     QTensor                       the quantized-weight container
     quantize_int8_rowwise(w)      load-time per-row weight quantization
     act_and_mul(x, act), rmsnorm(x, w, eps, residual=, unit_offset=)
@@ -23,6 +24,8 @@ named `fni8-serve_amd`; it is imported as `fni8serve_amd`.
 from .ops import (  # noqa: F401
     act_and_mul,
     act_and_mul_quant,
+    gemm_quantized,
+    gemm_w4a8,
     gemm_w8a8,
     gemm_w8a8_grouped,
     linear,
@@ -61,5 +64,6 @@ __all__ = [
     "Qwen3MLP", "SparseMoE", "LMHead", "NF4_CODEBOOK", "to_qtensor", "merge_qtensor",
     "qkv_weight", "gate_up_weight", "save_fni8", "FQWriter", "FQReader", "load_fni8_checkpoint",
     "load_fni8_state_dict", "checkpoint_info", "act_and_mul", "act_and_mul_quant", "rmsnorm",
-    "rmsnorm_quant", "RMSNorm", "SiluAndMul", "GeluAndMul", "get_act_and_mul",
+    "rmsnorm_quant", "RMSNorm", "SiluAndMul", "GeluAndMul", "get_act_and_mul", "gemm_w4a8",
+    "gemm_quantized",
 ]

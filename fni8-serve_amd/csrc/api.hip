@@ -69,6 +69,23 @@ int check_gemm_shape(int64_t M, int64_t K, int64_t N) {
     return FNI8_OK;
 }
 
+int check_w4a8(int64_t M, int64_t K, int64_t N, int64_t G, const uint8_t* w, const float* ws,
+               const void* bias, const void* y, int64_t ldy) {
+    REQUIRE(w && ws && y, FNI8_ERR_NULL, "w, ws and y are required");
+    REQUIRE(M >= 0 && M < kMaxDim && N > 0 && N < kMaxDim && K > 0 && K < kMaxDim,
+            FNI8_ERR_SHAPE, "M=%lld N=%lld K=%lld out of range", (long long)M, (long long)N,
+            (long long)K);
+    REQUIRE(G == 32 || G == 64 || G == 128 || G == 256, FNI8_ERR_SHAPE,
+            "group size %lld not supported (32, 64, 128, 256)", (long long)G);
+    REQUIRE(K % 32 == 0 && K % G == 0, FNI8_ERR_SHAPE,
+            "K=%lld must be a multiple of 32 and of the group size %lld", (long long)K,
+            (long long)G);
+    REQUIRE(ldy >= N, FNI8_ERR_STRIDE, "ldy=%lld < N=%lld", (long long)ldy, (long long)N);
+    REQUIRE(aligned(w, 16) && aligned(ws, 4) && aligned(bias, 2) && aligned(y, 2),
+            FNI8_ERR_ALIGN, "w must be 16-byte aligned; ws, bias, y element-aligned");
+    return FNI8_OK;
+}
+
 int check_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr,
                   const void* weight, float eps, int64_t M, int64_t K, int64_t ldo,
                   const void* residual_out, int64_t ldro) {
@@ -234,6 +251,45 @@ int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
     if (rc) return rc;
     return fni8h::launch_moe_combine((const uint16_t*)y_sorted, H, topi, (const uint16_t*)topw,
                                      pos, T, k, (uint16_t*)out, (hipStream_t)stream);
+}
+
+int fni8_gemm_w4a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                   const uint8_t* w, const float* ws, int64_t N, int64_t G, const void* bias,
+                   void* y, int64_t ldy, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(xq && xs, FNI8_ERR_NULL, "xq and xs are required");
+    int rc = check_w4a8(M, K, N, G, w, ws, bias, y, ldy);
+    if (rc) return rc;
+    REQUIRE(ldq >= K, FNI8_ERR_STRIDE, "ldq=%lld < K=%lld", (long long)ldq, (long long)K);
+    REQUIRE(ldq % 16 == 0 && aligned(xq, 16) && aligned(xs, 4), FNI8_ERR_ALIGN,
+            "xq rows must be 16-byte aligned");
+    rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_gemm_w4a8(xq, ldq, xs, M, K, w, ws, N, G, (const uint16_t*)bias,
+                                   (uint16_t*)y, ldy, (hipStream_t)stream);
+}
+
+int fni8_linear_w4a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const uint8_t* w,
+                         const float* ws, int64_t N, int64_t G, const void* bias, void* y,
+                         int64_t ldy, int8_t* xq, float* xs, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(x && xq && xs, FNI8_ERR_NULL, "x, xq and xs are required");
+    int rc = check_w4a8(M, K, N, G, w, ws, bias, y, ldy);
+    if (rc) return rc;
+    REQUIRE(ldx >= K, FNI8_ERR_STRIDE, "ldx=%lld < K=%lld", (long long)ldx, (long long)K);
+    REQUIRE(aligned(x, 2) && aligned(xq, 16) && aligned(xs, 4), FNI8_ERR_ALIGN,
+            "x, xq or xs misaligned");
+    rc = check_device();
+    if (rc) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    // decode sizes: one launch, the quantization fused into the stream kernel
+    rc = fni8h::launch_linear_w4a8_fused((const uint16_t*)x, ldx, M, K, w, ws, N, G,
+                                         (const uint16_t*)bias, (uint16_t*)y, ldy, xq, xs, st);
+    if (rc != 1) return rc;
+    rc = fni8h::launch_quant_rowwise((const uint16_t*)x, M, K, ldx, xq, K, xs, st);
+    if (rc) return rc;
+    return fni8h::launch_gemm_w4a8(xq, K, xs, M, K, w, ws, N, G, (const uint16_t*)bias,
+                                   (uint16_t*)y, ldy, st);
 }
 
 int fni8_moe_route(const float* logits, int64_t T, int64_t E, int64_t ldl, int scoring,

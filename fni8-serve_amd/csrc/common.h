@@ -272,6 +272,14 @@ int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* res, int64_t 
                    const uint16_t* w, float eps, int unit, int64_t M, int64_t K, uint16_t* out,
                    int64_t ldo, uint16_t* res_out, int64_t ldro, int8_t* q, int64_t ldq,
                    float* s, hipStream_t st);
+int launch_gemm_w4a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                     const uint8_t* w, const float* ws, int64_t N, int64_t G,
+                     const uint16_t* bias, uint16_t* y, int64_t ldy, hipStream_t st);
+// W4A8 decode (M <= 4) with the quantization fused in; 1 when not taken.
+int launch_linear_w4a8_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t K,
+                             const uint8_t* w, const float* ws, int64_t N, int64_t G,
+                             const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
+                             float* xs_out, hipStream_t st);
 int launch_moe_route(const float* logits, int64_t ldl, int64_t T, int64_t E, int scoring,
                      const float* bias, int64_t groups, int64_t topk_group, int64_t k, int renorm,
                      float scale, uint16_t* topw, int32_t* topi, hipStream_t st);

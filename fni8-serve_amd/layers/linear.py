@@ -9,14 +9,13 @@ fni8serve/layers/linear.py:28-71:
     _dequant_weight(qt)                          (linear.py:28-46)
     NF4_CODEBOOK                                 (linear.py:22-25)
 
-forward(x) dispatch follows linear.py:58-71: a per_row_i8 weight with x on the
-GPU runs `ops.linear` (per-token quant + int8 MFMA GEMM + fused epilogue); a
-CPU x runs the reference's numerically-correct fp16 fallback (dequantize the
-weight, F.linear), which is the reference's documented CPU behaviour.  On the
-GPU there is no fallback for per_row_i8: a missing library raises.  The W4A8
-`per_group_i4` int4 GPU kernel is not part of this build and raises
-NotImplementedError; NF4 weights take the dequant path on either device, as
-in the reference (linear.py:11-12, :65).
+forward(x) dispatch follows linear.py:58-71: a per_row_i8 (W8A8) or
+per_group_i4 int4 (W4A8) weight with x on the GPU runs `ops.linear`
+(per-token quant + int8 GEMM + fused epilogue); a CPU x runs the reference's
+numerically-correct fp16 fallback (dequantize the weight, F.linear), which is
+the reference's documented CPU behaviour.  On the GPU there is no fallback for
+those schemes: a missing library raises.  NF4 weights take the dequant path on
+either device, as in the reference (linear.py:11-12, :65).
 """
 from __future__ import annotations
 
@@ -65,15 +64,16 @@ class LinearW8A8(nn.Module):
         self.in_features = weight.data.shape[1] * (2 if weight.scheme == "per_group_i4" else 1)
 
     def _int8_ok(self, x: torch.Tensor) -> bool:
-        """The int8 kernels run for GPU activations and per_row_i8 weights
-        (the W8A8 half of linear.py:58-65)."""
-        return x.is_cuda and self.weight.scheme == "per_row_i8"
+        """The int8 kernels run for GPU activations with per_row_i8 weights
+        (W8A8) or per_group_i4 int4 weights (W4A8) -- linear.py:58-65."""
+        if not x.is_cuda:
+            return False
+        qt = self.weight
+        return qt.scheme == "per_row_i8" or (qt.scheme == "per_group_i4" and qt.codebook == "int4")
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self._int8_ok(x):
             return ops.linear(x, self.weight, bias=self.bias)
         qt = self.weight
-        if x.is_cuda and qt.scheme == "per_group_i4" and qt.codebook == "int4":
-            raise NotImplementedError("W4A8 (per_group_i4 int4) GPU kernel is not built")
         w = _dequant_weight(qt).to(x.dtype)    # reference fallback: CPU tensors, NF4
         return torch.nn.functional.linear(x, w, self.bias)

@@ -41,10 +41,10 @@ class GatedMLP(nn.Module):
         act = fused_act(self.act_fn)
         rows = x.numel() // max(x.shape[-1], 1)
         if (act is not None and rows >= FUSE_MIN_ROWS and self.gate_up_proj._int8_ok(x)
-                and self.down_proj.weight.scheme == "per_row_i8"):
+                and self.down_proj._int8_ok(x)):
             h = self.gate_up_proj(x)
             xq, xs = ops.act_and_mul_quant(h, act)
-            y = ops.gemm_w8a8(xq, xs, self.down_proj.weight, self.down_proj.bias)
+            y = ops.gemm_quantized(xq, xs, self.down_proj.weight, self.down_proj.bias)
             return y.reshape(*x.shape[:-1], y.shape[-1])
         return self.down_proj(self.act_fn(self.gate_up_proj(x)))
 

@@ -77,10 +77,56 @@ def _check_bias(bias: torch.Tensor | None, N: int):
     return bias.reshape(-1).contiguous()
 
 
+W4_GROUPS = (32, 64, 128, 256)
+
+
+def _check_weight_i4(qt: QTensor, K: int):
+    """per_group_i4 int4 weight (fni8serve/convert.py:69-79): packed uint8
+    [N, K/2], fp32 scales [N, K/G]."""
+    if qt.codebook != "int4":
+        raise ValueError(f"the W4A8 kernel needs the int4 codebook (got {qt.codebook!r}); "
+                         "NF4 weights take the dequantize path")
+    w, s, G = qt.data, qt.scale, qt.group_size
+    if w.dtype != torch.uint8 or w.dim() != 2 or not w.is_contiguous():
+        raise ValueError("per_group_i4 data must be a contiguous uint8 [N, K/2] tensor")
+    if 2 * w.shape[1] != K:
+        raise ValueError(f"in_features mismatch: x has K={K}, weight packs {2 * w.shape[1]}")
+    if G not in W4_GROUPS or K % G or K % 32:
+        raise ValueError(f"group size {G} with K={K} not supported (G in {W4_GROUPS}, "
+                         "dividing K; K a multiple of 32)")
+    N = w.shape[0]
+    if s is None or s.dtype != torch.float32 or s.numel() != N * (K // G) or not s.is_contiguous():
+        raise ValueError("per_group_i4 scale must be a contiguous fp32 tensor of N * K/G entries")
+    return w, s.reshape(N, K // G), G
+
+
+def _linear_w4a8(x, qt, bias):
+    K = x.shape[-1]
+    w, ws, G = _check_weight_i4(qt, K)
+    N = w.shape[0]
+    bias = _check_bias(bias, N)
+    dev = _require_cuda("linear", x, w, ws, bias)
+    if x.dtype != _f16:
+        raise ValueError(f"linear expects fp16 activations (got {x.dtype})")
+    x2, ldx = _rows(x, K)
+    M = x2.shape[0]
+    y = torch.empty((*x.shape[:-1], N), dtype=_f16, device=dev)
+    xq = torch.empty((M, K), dtype=torch.int8, device=dev)
+    xs = torch.empty((M,), dtype=torch.float32, device=dev)
+    if M:
+        with torch.cuda.device(dev):
+            _lib.call("fni8_linear_w4a8_f16", _ptr(x2), ldx, M, K, _ptr(w), _ptr(ws), N, G,
+                      _ptr(bias), _ptr(y), N, _ptr(xq), _ptr(xs), _stream(dev))
+    return y, xq, xs, None
+
+
 def linear_with_intermediates(x: torch.Tensor, qt: QTensor, bias: torch.Tensor | None = None,
                               want_acc: bool = False):
     """`linear` that also returns the quantized activations, their scales and
-    (if want_acc) the int32 accumulators: (y, xq [M, K], xs [M], acc [M, N] | None)."""
+    (if want_acc) the int32 accumulators: (y, xq [M, K], xs [M], acc [M, N] | None).
+    For per_group_i4 weights the accumulators are per group and not returned."""
+    if qt.scheme == "per_group_i4":
+        return _linear_w4a8(x, qt, bias)
     K = x.shape[-1]
     w, ws = _check_weight(qt, K)
     N = w.shape[0]
@@ -103,7 +149,8 @@ def linear_with_intermediates(x: torch.Tensor, qt: QTensor, bias: torch.Tensor |
 
 
 def linear(x: torch.Tensor, qt: QTensor, bias: torch.Tensor | None = None) -> torch.Tensor:
-    """fni8.linear(x, qt, bias=None): x fp16 [..., K] on the GPU -> fp16 [..., N]."""
+    """fni8.linear(x, qt, bias=None): x fp16 [..., K] on the GPU -> fp16 [..., N],
+    for per_row_i8 (W8A8) and per_group_i4 int4 (W4A8) weights."""
     return linear_with_intermediates(x, qt, bias)[0]
 
 
@@ -145,6 +192,38 @@ def gemm_w8a8(xq: torch.Tensor, xs: torch.Tensor, qt: QTensor, bias: torch.Tenso
             _lib.call("fni8_gemm_w8a8", _ptr(xq), ldq, _ptr(xs), M, K, _ptr(w), _ptr(ws), N,
                       _ptr(bias), _ptr(y), N, _ptr(acc), _stream(dev))
     return (y, acc) if want_acc else y
+
+
+def gemm_w4a8(xq: torch.Tensor, xs: torch.Tensor, qt: QTensor,
+              bias: torch.Tensor | None = None) -> torch.Tensor:
+    """`gemm_w4a8` on already-quantized activations: xq int8 [M, K], xs fp32 [M]
+    and a per_group_i4 int4 QTensor -> y fp16 [M, N]."""
+    if xq.dtype != torch.int8 or xq.dim() != 2 or xq.stride(1) != 1:
+        raise ValueError("xq must be int8 [M, K] with unit inner stride")
+    M, K = xq.shape
+    w, ws, G = _check_weight_i4(qt, K)
+    N = w.shape[0]
+    bias = _check_bias(bias, N)
+    if xs.dtype != torch.float32 or xs.numel() != M or not xs.is_contiguous():
+        raise ValueError("xs must be a contiguous fp32 tensor with M entries")
+    dev = _require_cuda("gemm_w4a8", xq, xs, w, ws, bias)
+    y = torch.empty((M, N), dtype=_f16, device=dev)
+    if M:
+        ldq = xq.stride(0) if M > 1 else K
+        if ldq % 16 or xq.data_ptr() % 16:
+            xq, ldq = xq.contiguous(), K
+        with torch.cuda.device(dev):
+            _lib.call("fni8_gemm_w4a8", _ptr(xq), ldq, _ptr(xs), M, K, _ptr(w), _ptr(ws), N, G,
+                      _ptr(bias), _ptr(y), N, _stream(dev))
+    return y
+
+
+def gemm_quantized(xq: torch.Tensor, xs: torch.Tensor, qt: QTensor,
+                   bias: torch.Tensor | None = None) -> torch.Tensor:
+    """The GEMM of `linear` for either weight scheme on pre-quantized activations."""
+    if qt.scheme == "per_group_i4":
+        return gemm_w4a8(xq, xs, qt, bias)
+    return gemm_w8a8(xq, xs, qt, bias)
 
 
 def moe_sort(topi: torch.Tensor, num_experts: int):

@@ -142,6 +142,36 @@ int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
                          const void* topw, const int32_t* pos, int64_t T, int64_t k,
                          void* out, void* stream);
 
+/*
+ * W4A8 GEMM: int8 activations against per_group_i4 int4 weights, `gemm_w4a8`
+ * (replaces the GEMM half of fni8.linear for int4 QTensors,
+ * fni8serve/layers/linear.py:9 and :63-65; weight format
+ * fni8serve/convert.py:69-79).
+ *   xq        int8 [M, K], row stride ldq bytes (a multiple of 16, base 16-byte
+ *             aligned); xs fp32 [M]
+ *   w         uint8 [N, K/2]: code k of row n in byte k/2, low nibble for even
+ *             k, 4-bit two's complement; 16-byte aligned
+ *   ws        fp32 [N, K/G]: one scale per group of G consecutive k
+ *   G         32, 64, 128 or 256, dividing K; K a multiple of 32
+ *   bias      fp16 [N] or NULL; y fp16 [M, N], row stride ldy
+ * Arithmetic: per group the exact int32 sum acc_g; accf = fma(acc_g, ws[n, g],
+ * accf) in ascending g from +0; y = fp16(accf * xs[m] (+ bias[n])).
+ */
+int fni8_gemm_w4a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                   const uint8_t* w, const float* ws, int64_t N, int64_t G, const void* bias,
+                   void* y, int64_t ldy, void* stream);
+
+/*
+ * The whole W4A8 linear, `fni8.linear(x, qt, bias)` for a per_group_i4 int4
+ * QTensor (replaces fni8serve/layers/linear.py:69 on that scheme): per-token
+ * quantization of x as in fni8_quantize_rowwise_f16, then fni8_gemm_w4a8.
+ *   x      fp16 [M, K], row stride ldx; xq int8 [M, K] (row stride K) and
+ *          xs fp32 [M] receive the quantized activations
+ */
+int fni8_linear_w4a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const uint8_t* w,
+                         const float* ws, int64_t N, int64_t G, const void* bias, void* y,
+                         int64_t ldy, int8_t* xq, float* xs, void* stream);
+
 /* Router scoring functions of fni8_moe_route. */
 enum {
     FNI8_SCORE_SOFTMAX = 0, /* softmax over all experts (Qwen, Hunyuan, MiniMax) */

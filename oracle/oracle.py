@@ -30,6 +30,12 @@ parity pinning (how each function is checked, in tests/test_oracle.py):
       sorting (value desc, index asc), the reference's torch routing
       (fni8serve/models/moe.py:62-97) on the CPU: same experts, weights within
       1 fp16 ulp; known answers (ties, groups, NaN rows, renormalisation).
+  gemm_w4a8 / linear_w4a8_f16 (w4a8_oracle.c) -- the group sums exact against
+      numpy integer matmuls over codes packed by the reference's own formula
+      (fni8serve/convert.py:72-73) and unpacked as fni8serve/layers/linear.py:32-40
+      does; outputs against the float64 closed form within the fp32 fold's error
+      bound; the reference's CPU fallback (dequantize, F.linear) by cosine; the
+      ascending-group fold order on a case that exposes it.
   sumsq_fixed / rmsnorm_f16 -- math.fsum error bound, exact known answers,
       float64 closed form, torch's eager RMSNorm (fni8serve/layers/norm.py:37-58)
       and torch's fp16 residual add bit for bit, unit-offset identity.
@@ -82,6 +88,8 @@ def _load():
     lib.oracle_exp_cw_n.argtypes = [P, P, I]
     lib.oracle_act_f32_n.argtypes = [P, P, I, C]
     lib.oracle_moe_route.argtypes = [P, I, I, I, C, P, I, I, I, C, F, P, P]
+    lib.oracle_gemm_w4a8.argtypes = [P, P, I, I, P, P, I, I, P, P, P]
+    lib.oracle_linear_w4a8_f16.argtypes = [P, I, I, P, P, I, I, P, P, P, P]
     lib.oracle_sumsq_fixed.restype = F
     lib.oracle_sumsq_fixed.argtypes = [P, I]
     lib.oracle_rmsnorm_f16.argtypes = [P, I, P, I, P, F, C, I, I, P, I, P, I, P]
@@ -91,7 +99,8 @@ def _load():
                "oracle_grouped_w8a8_f16", "oracle_moe_combine_f16",
                "oracle_quant_identity_check", "oracle_act_and_mul_f16",
                "oracle_act_and_mul_quant_f16", "oracle_rmsnorm_f16", "oracle_rmsnorm_quant_f16",
-               "oracle_exp_cw_n", "oracle_act_f32_n", "oracle_moe_route"):
+               "oracle_exp_cw_n", "oracle_act_f32_n", "oracle_moe_route", "oracle_gemm_w4a8",
+               "oracle_linear_w4a8_f16"):
         getattr(lib, fn).restype = None
     _lib = lib
     return lib
@@ -318,3 +327,36 @@ def moe_route(logits, k, scoring="softmax", bias=None, groups=0, topk_group=0, r
     _load().oracle_moe_route(_p(lg), T, E, E, SCORES[scoring], _p(b), groups, topk_group, k,
                              int(bool(renorm)), float(np.float32(scale)), _p(topw), _p(topi))
     return topw, topi
+
+
+def gemm_w4a8(xq, xs, w_packed, ws, group_size, bias=None, want_groups=False):
+    """xq int8 [M, K], xs fp32 [M]; w_packed uint8 [N, K/2]; ws fp32 [N, K/G]
+    -> y fp16 [M, N] (and the int32 group sums [M, N, K/G])."""
+    xq = _c(xq, np.int8)
+    xs = _c(xs, np.float32)
+    w = _c(w_packed, np.uint8)
+    ws = _c(ws, np.float32)
+    M, K = xq.shape
+    N = w.shape[0]
+    b = None if bias is None else _c(bias, np.float16)
+    y = np.empty((M, N), np.float16)
+    ga = np.empty((M, N, K // group_size), np.int32) if want_groups else None
+    _load().oracle_gemm_w4a8(_p(xq), _p(xs), M, K, _p(w), _p(ws), N, group_size, _p(b), _p(y),
+                             _p(ga))
+    return (y, ga) if want_groups else y
+
+
+def linear_w4a8_f16(x, w_packed, ws, group_size, bias=None):
+    """Whole W4A8 linear: returns (y fp16 [M, N], xq int8, xs fp32)."""
+    x = _c(x, np.float16)
+    w = _c(w_packed, np.uint8)
+    ws = _c(ws, np.float32)
+    M, K = x.shape
+    N = w.shape[0]
+    b = None if bias is None else _c(bias, np.float16)
+    y = np.empty((M, N), np.float16)
+    xq = np.empty((M, K), np.int8)
+    xs = np.empty((M,), np.float32)
+    _load().oracle_linear_w4a8_f16(_p(x), M, K, _p(w), _p(ws), N, group_size, _p(b), _p(y),
+                                   _p(xq), _p(xs))
+    return y, xq, xs
