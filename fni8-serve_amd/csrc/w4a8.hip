@@ -361,6 +361,253 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_stream_kernel(
     }
 }
 
+// ---- decode on MFMA: int8 activations, up to 64 tokens -----------------------
+//
+// The W8A8 decode layout with packed weights.  A workgroup owns 16*NB weight
+// rows.  One load instruction covers 8 rows x 128 packed bytes (a "slab" of
+// 256 codes per row), or 8 tokens x 128 activation bytes, so every load
+// touches whole cache lines.  Both go through a wave-private LDS tile
+// (16-byte chunks XOR-swizzled by row, conflict-free both ways) and come back
+// in the operand layout of v_mfma_i32_16x16x64_i8.
+//
+// Unpacking: a lane's B operand for one 64-code k-block is 16 codes of one
+// row in natural k order, 8 packed bytes.  Each nibble is moved to the high
+// half of its byte, where the byte reads as int8 16 * code exactly (the nibble
+// is two's complement).  The MFMA then sums 16 * acc_g, and an arithmetic
+// shift by 4 recovers acc_g exactly (|acc_g| <= 127 * 8 * 256).  Per packed
+// dword that is one shift, two v_perm and two masks, with no sign-extension.
+//
+// The fold needs each group's exact sum in ascending g, while the waves of a
+// workgroup split K.  They do so in rounds: round r covers WAVES*SB slabs and
+// wave w the SB slabs from (r*WAVES + w)*SB.  Each wave writes its groups'
+// int32 sums to LDS.  After one barrier, every thread folds its own output
+// elements through the round's groups in order.  The group-sum area is double
+// buffered, so one barrier per round suffices: a wave writes round r+2's sums
+// only after the barrier of round r+1, and every thread reaches that barrier
+// after folding round r.
+__device__ __forceinline__ int swz(int row, int chunk) {
+    return ((chunk ^ (row & 7) ^ ((row >> 3) & 7)) & 7) * 16;
+}
+
+// Waits for this wave's LDS traffic, then meets the other waves.  Unlike
+// __syncthreads it leaves the outstanding global loads (the next round's
+// weights) in flight.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// 8 packed bytes (16 codes) -> 16 int8 in natural k order, each 16 * code.
+__device__ __forceinline__ i32x4 unpack16x16(uint32_t lo, uint32_t hi) {
+    const uint32_t sl = lo << 4, sh = hi << 4;
+    i32x4 r;
+    r[0] = (int)(__builtin_amdgcn_perm(lo, sl, 0x05010400u) & 0xf0f0f0f0u);
+    r[1] = (int)(__builtin_amdgcn_perm(lo, sl, 0x07030602u) & 0xf0f0f0f0u);
+    r[2] = (int)(__builtin_amdgcn_perm(hi, sh, 0x05010400u) & 0xf0f0f0f0u);
+    r[3] = (int)(__builtin_amdgcn_perm(hi, sh, 0x07030602u) & 0xf0f0f0f0u);
+    return r;
+}
+
+template <int MT, int NB, int WAVES, int SB, int G>
+__global__ __launch_bounds__(WAVES * 64) void w4a8_mfma_kernel(
+    const int8_t* __restrict__ xq, int64_t ldx, const float* __restrict__ xs, int M, int K,
+    const uint8_t* __restrict__ w, const float* __restrict__ ws, int N,
+    const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy) {
+    constexpr int ROWS = 16 * NB, TOK = 16 * MT;
+    constexpr int TILE = (ROWS + 2 * TOK) * 128;  // weight rows, then 2 activation halves per token
+    constexpr int KBG = G / 64;                    // MFMA k-blocks per group
+    constexpr int GPS = 256 / G;                   // groups per slab
+    constexpr int GPR = WAVES * SB * GPS;          // groups per round
+    constexpr int EL = MT * NB * 256;              // output elements of the workgroup
+    constexpr int EPT = EL / (WAVES * 64);         // folded by each thread
+    // WAVES in {1, 2, 4}: then (k*WAVES + wave) / 4 == (k*WAVES) / 4 for every
+    // wave, which keeps each thread's weight-row block a compile-time constant
+    static_assert(G >= 64 && G <= 256 && (WAVES == 1 || WAVES == 2 || WAVES == 4) &&
+                      EL % (WAVES * 64) == 0, "w4a8 mfma shape");
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int32_t* gs = reinterpret_cast<int32_t*>(smem + WAVES * SB * TILE);  // [2][GPR][EL]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * ROWS;
+    const int ng = K / G;
+    const int rounds = (K >> 8) / (WAVES * SB);
+    const int rq = lane >> 3, c = lane & 7, r = lane & 15, g = lane >> 4;
+    const int64_t kh = K >> 1;
+
+    // load lanes: weight row h*8 + rq (rows past N repeat row N-1, never
+    // stored), activation token h*8 + rq (past M repeats M-1), chunk c
+    const uint8_t* wsrc[2 * NB];
+    int woff[2 * NB];
+#pragma unroll
+    for (int h = 0; h < 2 * NB; h++) {
+        const int row = h * 8 + rq;
+        const int n = n0 + row < N ? n0 + row : N - 1;
+        wsrc[h] = w + (int64_t)n * kh + (int64_t)wave * SB * 128 + c * 16;
+        woff[h] = row * 128 + swz(row, c);
+    }
+    const int8_t* xsrc[2 * MT];
+    int xoff[2 * MT][2];
+#pragma unroll
+    for (int h = 0; h < 2 * MT; h++) {
+        const int tok = h * 8 + rq;
+        xsrc[h] = xq + (int64_t)(tok < M ? tok : M - 1) * ldx + (int64_t)wave * SB * 256 + c * 16;
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const int row = ROWS + p * TOK + tok;
+            xoff[h][p] = row * 128 + swz(row, c);
+        }
+    }
+    // operand lanes: k-block j of the slab is codes 64j..64j+63; lane (r, g)
+    // holds codes 64j + 16g .. +15 of weight row / token r
+    int boff[NB][4], aoff[MT][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int b = 0; b < NB; b++) {
+            const int row = b * 16 + r;
+            boff[b][j] = row * 128 + swz(row, 2 * j + (g >> 1)) + 8 * (g & 1);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const int row = ROWS + (j >> 1) * TOK + mt * 16 + r;
+            aoff[mt][j] = row * 128 + swz(row, 4 * (j & 1) + g);
+        }
+    }
+
+    i32x4 wa[SB][2 * NB], wb[SB][2 * NB];
+    i32x4 xa[SB][4 * MT], xb[SB][4 * MT];
+    auto load = [&](i32x4 (&dw)[SB][2 * NB], i32x4 (&dx)[SB][4 * MT], int rd) {
+        const int64_t s = (int64_t)rd * WAVES * SB;
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++)
+                dw[j][h] = __builtin_nontemporal_load(
+                    reinterpret_cast<const i32x4*>(wsrc[h] + (s + j) * 128));
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < 2 * MT; h++)
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    dx[j][2 * h + p] =
+                        *reinterpret_cast<const i32x4*>(xsrc[h] + (s + j) * 256 + p * 128);
+    };
+
+    int8_t* st = smem + wave * (SB * TILE);
+    auto compute = [&](const i32x4 (&wv)[SB][2 * NB], const i32x4 (&xv)[SB][4 * MT], int32_t* gsb) {
+        // The tile is private to the wave and LDS executes a wave's accesses in
+        // order; the barriers only keep the compiler from reordering across them.
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + woff[h]) = wv[j][h];
+#pragma unroll
+            for (int h = 0; h < 2 * MT; h++)
+#pragma unroll
+                for (int p = 0; p < 2; p++)
+                    *reinterpret_cast<i32x4*>(st + j * TILE + xoff[h][p]) = xv[j][2 * h + p];
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+#pragma unroll
+            for (int gj = 0; gj < GPS; gj++) {
+                i32x4 acc[MT][NB];
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++) acc[mt][b] = i32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int kb = 0; kb < KBG; kb++) {
+                    const int jb = gj * KBG + kb;
+                    i32x4 bf[NB], af[MT];
+#pragma unroll
+                    for (int b = 0; b < NB; b++) {
+                        const uint2 pk = *reinterpret_cast<const uint2*>(st + j * TILE + boff[b][jb]);
+                        bf[b] = unpack16x16(pk.x, pk.y);
+                    }
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+                        af[mt] = *reinterpret_cast<const i32x4*>(st + j * TILE + aoff[mt][jb]);
+#pragma unroll
+                    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                        for (int b = 0; b < NB; b++) acc[mt][b] = fni8::mfma_i8(af[mt], bf[b], acc[mt][b]);
+                }
+                const int gl = (wave * SB + j) * GPS + gj;
+#pragma unroll
+                for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+                    for (int b = 0; b < NB; b++)
+                        *reinterpret_cast<i32x4*>(gsb + gl * EL + ((mt * NB + b) * 64 + lane) * 4) =
+                            acc[mt][b];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    };
+
+    // fold ownership: element e = (k*WAVES + wave)*64 + lane of the MFMA
+    // result layout [MT*NB][64 lanes][4]: block (k*WAVES + wave) / 4, weight
+    // row lane / 4 of it, token 4 * ((k*WAVES + wave) % 4) + lane % 4
+    const float* wrow[NB];
+#pragma unroll
+    for (int b = 0; b < NB; b++) {
+        const int n = n0 + b * 16 + (lane >> 2);
+        wrow[b] = ws + (int64_t)(n < N ? n : N - 1) * ng;
+    }
+    float accf[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; k++) accf[k] = 0.0f;
+    float wsv[NB][GPR];
+    auto fold = [&](const int32_t* gsb) {
+#pragma unroll
+        for (int gl = 0; gl < GPR; gl++)
+#pragma unroll
+            for (int k = 0; k < EPT; k++) {
+                const int b = ((k * WAVES) >> 2) % NB;  // (k*WAVES + wave) / 4: no carry
+                const int32_t v = gsb[gl * EL + (k * WAVES + wave) * 64 + lane];
+                accf[k] = __builtin_fmaf((float)(v >> 4), wsv[b][gl], accf[k]);
+            }
+    };
+
+    load(wa, xa, 0);
+    for (int rd = 0; rd < rounds; rd++) {
+        if (rd + 1 < rounds) load(wb, xb, rd + 1);
+#pragma unroll
+        for (int b = 0; b < NB; b++)
+#pragma unroll
+            for (int gl = 0; gl < GPR; gl++) wsv[b][gl] = wrow[b][rd * GPR + gl];
+        int32_t* gsb = gs + (rd & 1) * GPR * EL;
+        compute(wa, xa, gsb);
+        lds_barrier();
+        fold(gsb);
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+#pragma unroll
+            for (int h = 0; h < 2 * NB; h++) wa[j][h] = wb[j][h];
+#pragma unroll
+            for (int h = 0; h < 4 * MT; h++) xa[j][h] = xb[j][h];
+        }
+    }
+
+#pragma unroll
+    for (int k = 0; k < EPT; k++) {
+        const int mb = (k * WAVES) >> 2;
+        const int n = n0 + (mb % NB) * 16 + (lane >> 2);
+        const int m = (mb / NB) * 16 + 4 * (((k * WAVES) & 3) + wave) + (lane & 3);
+        if (m < M && n < N) {
+            float v = accf[k] * xs[m];
+            if (bias) v = v + fni8::h2f(bias[n]);
+            y[(int64_t)m * ldy + n] = fni8::f2h(v);
+        }
+    }
+}
+
 // ---- prefill: MFMA tile, group-wise fp32 fold --------------------------------
 //
 // Workgroup of 4 waves (2 x 2) over a BM x BN tile; each wave a (BM/2) x (BN/2)
@@ -531,6 +778,7 @@ int launch_error(const char* what) {
 
 constexpr size_t kLdsBytes = 160 * 1024;
 constexpr int64_t kSliceMaxM = 16;  // rows up to which the sliced GEMV beats the tile grid
+constexpr int64_t kMfmaMinM = 4;    // from this many rows on the MFMA decode kernel runs first
 
 // Static LDS of w4a8_gemv_kernel<MT, CPG>: the per-wave group sums.
 template <int MT, int CPG>
@@ -608,6 +856,86 @@ int stream_launch(const void* x, int64_t ldx, const float* xs_in, int64_t M, int
     return launch_error("w4a8 stream");
 }
 
+// LDS bytes of w4a8_mfma_kernel: the wave tiles, then the two group-sum areas.
+template <int MT, int NB, int WAVES, int SB, int G>
+constexpr size_t kMfmaLds = (size_t)WAVES * SB * (16 * NB + 32 * MT) * 128 +
+                            (size_t)2 * WAVES * SB * (256 / G) * MT * NB * 256 * 4;
+
+template <int MT, int NB, int WAVES, int SB, int G>
+int mfma_launch(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                const uint8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
+                int64_t ldy, hipStream_t st) {
+    constexpr size_t lds = kMfmaLds<MT, NB, WAVES, SB, G>;
+    if constexpr (lds > kLdsBytes) return 1;
+    if ((K >> 8) % (WAVES * SB) != 0) return 1;
+    auto kern = &w4a8_mfma_kernel<MT, NB, WAVES, SB, G>;
+    if constexpr (lds > 64 * 1024) {
+        static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)lds) == hipSuccess;
+        if (!ok) {
+            fni8h::set_error_detail("w4a8 mfma: cannot raise the LDS limit to %zu bytes", lds);
+            return FNI8_ERR_LAUNCH;
+        }
+    }
+    const dim3 grid((unsigned)((N + 16 * NB - 1) / (16 * NB)));
+    hipLaunchKernelGGL(kern, grid, dim3(WAVES * 64), lds, st, xq, ldq, xs, (int)M, (int)K, w, ws,
+                       (int)N, bias, y, ldy);
+    return launch_error("w4a8 mfma");
+}
+
+// Launch shape by token tiles and weight shape, measured on MI355X over the
+// Qwen3-8B linears at G = 128 (24 distinct weight copies per shape, weights
+// from HBM); other shapes take the first entry whose round divides K's slabs.
+template <int MT, int G>
+int mfma_table(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+               const uint8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
+               int64_t ldy, hipStream_t st) {
+#define FNI8_W4M(NB, WV, SB)                                                                 \
+    do {                                                                                     \
+        const int rc = mfma_launch<MT, NB, WV, SB, G>(xq, ldq, xs, M, K, w, ws, N, bias, y,  \
+                                                      ldy, st);                              \
+        if (rc != 1) return rc;                                                              \
+    } while (0)
+    const bool wide = N >= 16384, narrow = N <= 4096;
+    if constexpr (MT == 1) {
+        if (wide) FNI8_W4M(1, 2, 1);
+        FNI8_W4M(1, 4, 2);
+    } else if constexpr (MT == 2) {
+        if (narrow) FNI8_W4M(1, 4, 2);
+    } else {
+        if (!narrow) FNI8_W4M(1, 2, 1);
+    }
+    FNI8_W4M(1, 4, 1);
+    FNI8_W4M(1, 2, 1);
+    FNI8_W4M(1, 1, 1);
+#undef FNI8_W4M
+    return 1;
+}
+
+// 1 when the shape is not taken: group size 64..256, K a multiple of 256, at
+// most 64 tokens, 16-byte aligned activation rows.
+int mfma_dispatch(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                  const uint8_t* w, const float* ws, int64_t N, int64_t G, const uint16_t* bias,
+                  uint16_t* y, int64_t ldy, hipStream_t st) {
+    if (M < 1 || M > 64 || G < 64 || K % 256 != 0 || K > 65536) return 1;
+    if (ldq % 16 != 0 || ((uintptr_t)xq % 16) != 0 || ((uintptr_t)w % 16) != 0) return 1;
+    const int mt = (int)((M + 15) / 16);
+#define FNI8_W4M_G(MTV)                                                                         \
+    switch (G) {                                                                                \
+        case 64: return mfma_table<MTV, 64>(xq, ldq, xs, M, K, w, ws, N, bias, y, ldy, st);     \
+        case 128: return mfma_table<MTV, 128>(xq, ldq, xs, M, K, w, ws, N, bias, y, ldy, st);   \
+        default: return mfma_table<MTV, 256>(xq, ldq, xs, M, K, w, ws, N, bias, y, ldy, st);    \
+    }
+    switch (mt) {
+        case 1: FNI8_W4M_G(1)
+        case 2: FNI8_W4M_G(2)
+        case 3: FNI8_W4M_G(3)
+        default: FNI8_W4M_G(4)
+    }
+#undef FNI8_W4M_G
+}
+
 // 1 when the shape is not taken: K a multiple of 1024 (four waves of whole
 // 256-code slabs), at most 4 tokens, LDS within the limit.
 template <bool FUSED>
@@ -661,6 +989,10 @@ int launch_gemm_w4a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, 
                      const uint8_t* w, const float* ws, int64_t N, int64_t G,
                      const uint16_t* bias, uint16_t* y, int64_t ldy, hipStream_t st) {
     if (M == 0) return FNI8_OK;
+    if (M > kMfmaMinM) {
+        const int rc = mfma_dispatch(xq, ldq, xs, M, K, w, ws, N, G, bias, y, ldy, st);
+        if (rc != 1) return rc;
+    }
     // Up to kSliceMaxM rows: the streaming GEMV on slices of at most 4 rows (each
     // slice streams the weights again, still cheaper at these sizes than a tile
     // grid of N / 128 workgroups, too few to fill the chip).  The full-line

@@ -1,7 +1,8 @@
 """GPU parity of the W4A8 linear (per_group_i4 int4 weights) against the oracle
 (oracle/w4a8_oracle.c): int8 activations, fp32 scales and fp16 outputs bit for
-bit, on the decode GEMV (1-4 tokens) and the MFMA tile kernel (more tokens),
-every supported group size, Qwen3-8B's shapes and ragged ones.  Each output
+bit, on the decode GEMVs (1-4 tokens), the MFMA decode kernel (5-64 tokens)
+and the MFMA tile kernel (more tokens), every supported group size, Qwen3-8B's
+shapes and ragged ones.  Each output
 element depends only on its own activation row and weight row, so at full size
 the oracle checks sampled rows and columns.  Also the reference's own W4 seam
 test (tests/test_smoke.py:83-94: cosine against the fp16 dequantized weight)
@@ -141,3 +142,28 @@ def test_w4a8_prequantized_gemm_bitexact(pkg, M, G):
                        qt.scale.cpu().numpy(), G, bias=bias.cpu().numpy())
     assert np.array_equal(y.cpu().numpy().view(np.uint16), want.view(np.uint16))
     assert torch.equal(y, pkg.linear(x, qt, bias))
+
+
+@pytest.mark.parametrize("G", [64, 128, 256])
+@pytest.mark.parametrize("M", [5, 8, 16, 17, 31, 32, 33, 48, 63, 64])
+@pytest.mark.parametrize("K", [256, 512, 1536, 4096])
+def test_w4a8_mfma_decode_bitexact(pkg, M, K, G):
+    """5..64 tokens, group sizes 64..256: the MFMA decode kernel (waves split K
+    in rounds of slabs, exact group sums folded in order).  K = 256, 512 and
+    1536 take the one- and two-wave shapes, 4096 the four-wave ones; N is
+    ragged (not a multiple of 16 or 32 rows); every output element against
+    the oracle, bias on odd M."""
+    print(f"w4a8 mfma M={M} K={K} G={G}", flush=True)
+    N = 200 if K <= 1536 else 72
+    qt = _w4(pkg, N, K, G, seed=M * 11 + K + G)
+    bias = torch.randn(N, device="cuda").half() if M % 2 else None
+    _check(pkg, _x(M, K, seed=M * 13 + G), qt, bias)
+
+
+def test_w4a8_mfma_strided_rows(pkg):
+    """Activation rows with a stride (a view of a wider buffer)."""
+    M, K, N, G = 24, 2048, 96, 128
+    qt = _w4(pkg, N, K, G, seed=5)
+    big = _x(M, K + 256, seed=6)
+    x = big[:, 128:128 + K]
+    _check(pkg, x, qt, None)
