@@ -29,6 +29,113 @@ __device__ __forceinline__ i32x4 ld16(const int8_t* p) {
     return *reinterpret_cast<const i32x4*>(p);
 }
 
+// Barrier for the LDS stages: waits for this wave's LDS traffic only.  The
+// compiler's __syncthreads also waits for every outstanding global load, which
+// would drain the loads issued two steps ahead at every step.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// XCD-aware order of the dense tiles: consecutive workgroup ids land on
+// different XCDs, so each XCD gets a contiguous band of tiles, walked 8
+// m-tiles at a time.
+template <int BM, int BN>
+__device__ __forceinline__ void dense_tile(int M, int N, int& m0, int& m1, int& n0) {
+    const int ntiles_n = (N + BN - 1) / BN;
+    const int ntiles_m = (M + BM - 1) / BM;
+    const int total = ntiles_m * ntiles_n;
+    int bid = blockIdx.x;
+    if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
+    constexpr int GM = 8;
+    const int group = bid / (GM * ntiles_n);
+    const int first_m = group * GM;
+    const int gsize = min(ntiles_m - first_m, GM);
+    const int in_group = bid - group * GM * ntiles_n;
+    m0 = (first_m + in_group % gsize) * BM;
+    m1 = min(M, m0 + BM);
+    n0 = (in_group / gsize) * BN;
+}
+
+// Epilogue of the tile kernel (8 waves, 2 x 4): the accumulators go to
+// LDS as int32 (half the tile at a time), then every thread streams 16-byte
+// rows back, applies fp16(((float)acc * as[m]) * ws[n] (+ bias[n])) with a
+// wave-uniform row scale and writes 8 contiguous bytes per lane.  The caller
+// has finished with its LDS stages (a barrier before the call).
+template <int BM, int BN, bool GROUPED, bool WRITE_ACC, int FM = BM / 64, int FN = BN / 128>
+__device__ __forceinline__ void tile_epilogue(const i32x16 (&acc)[FM][FN], int8_t* smem, int tid,
+                                              int lane, int wm, int wn, int m0, int m1, int n0,
+                                              int N, const int32_t* __restrict__ row_index,
+                                              const float* __restrict__ as,
+                                              const float* __restrict__ wsexp,
+                                              const uint16_t* __restrict__ bexp,
+                                              uint16_t* __restrict__ y, int64_t ldy,
+                                              int32_t* __restrict__ acc_out) {
+    constexpr int NT = 512, WTN = BN / 4;
+    constexpr int HALF = BM / 2;          // rows staged per pass (one wave-row)
+    constexpr int OTS = BN + 8;           // int32 row stride of the staging tile
+    float* as_l = reinterpret_cast<float*>(smem);
+    float* ws_l = as_l + BM;
+    int32_t* ot = reinterpret_cast<int32_t*>(ws_l + BN);
+    for (int t = tid; t < BM; t += NT) {
+        const int mr = m0 + t;
+        float v = 0.f;
+        if (mr < m1) v = as[(GROUPED && row_index != nullptr) ? row_index[mr] : mr];
+        as_l[t] = v;
+    }
+    for (int t = tid; t < BN; t += NT) ws_l[t] = (n0 + t < N) ? wsexp[n0 + t] : 0.f;
+
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+        if (wm == pass) {
+            // lane l, register r of block (i, j): row 8*(r/4) + 4*(l/32) + r%4, col l%32
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        const int col = wn * WTN + j * 32 + (lane & 31);
+                        ot[row * OTS + col] = acc[i][j][r];
+                    }
+        }
+        __syncthreads();
+        // stream the staged half: BN/4 chunks of 4 columns per row; a wave covers
+        // whole rows, so the row scale is uniform across the wave
+        constexpr int CHR = BN / 4;
+        for (int c = tid; c < HALF * CHR; c += NT) {
+            const int rl = c / CHR, cl = (c % CHR) * 4;
+            const int row_t = pass * HALF + rl;
+            const int mr = m0 + row_t;
+            const int col = n0 + cl;
+            if (mr >= m1 || col >= N) continue;
+            const i32x4 a4 = *reinterpret_cast<const i32x4*>(ot + rl * OTS + cl);
+            const float asc = as_l[row_t];
+            uint16_t h[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float v = (float)a4[q] * asc;
+                v = v * ws_l[cl + q];
+                if (bexp != nullptr && col + q < N) v = v + fni8::h2f(bexp[col + q]);
+                h[q] = fni8::f2h(v);
+            }
+            uint16_t* yp = y + (int64_t)mr * ldy + col;
+            if (col + 3 < N && ((uintptr_t)yp & 7) == 0) {
+                uint2 pk;
+                pk.x = h[0] | ((uint32_t)h[1] << 16);
+                pk.y = h[2] | ((uint32_t)h[3] << 16);
+                *reinterpret_cast<uint2*>(yp) = pk;
+            } else {
+                for (int q = 0; q < 4 && col + q < N; q++) yp[q] = h[q];
+            }
+            if constexpr (WRITE_ACC) {
+                for (int q = 0; q < 4 && col + q < N; q++) acc_out[(int64_t)mr * N + col + q] = a4[q];
+            }
+        }
+        __syncthreads();
+    }
+}
+
 template <int BM, int BN, int BK, bool GROUPED, bool WRITE_ACC>
 __global__ __launch_bounds__(512) void gemm_tile32_kernel(
     const int8_t* __restrict__ aq, int64_t lda, const float* __restrict__ as,
@@ -49,7 +156,6 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-    const int ntiles_n = (N + BN - 1) / BN;
 
     int m0, m1, n0;
     const int8_t* wexp = w;
@@ -63,20 +169,7 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
         wsexp += (int64_t)e * N;
         if (bias) bexp += (int64_t)e * N;
     } else {
-        // XCD-aware order: consecutive ids land on different XCDs, so give each
-        // XCD a contiguous band of tiles, walked 8 m-tiles at a time.
-        const int ntiles_m = (M + BM - 1) / BM;
-        const int total = ntiles_m * ntiles_n;
-        int bid = blockIdx.x;
-        if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
-        constexpr int GM = 8;
-        const int group = bid / (GM * ntiles_n);
-        const int first_m = group * GM;
-        const int gsize = min(ntiles_m - first_m, GM);
-        const int in_group = bid - group * GM * ntiles_n;
-        m0 = (first_m + in_group % gsize) * BM;
-        m1 = min(M, m0 + BM);
-        n0 = (in_group / gsize) * BN;
+        dense_tile<BM, BN>(M, N, m0, m1, n0);
     }
 
     // Global sources of this thread's chunks; rows past the end are clamped to
@@ -160,87 +253,25 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
     gload(0, C0{});
     gload(1, C1{});
     sstore(C0{}, C0{});
-    __syncthreads();
+    lds_barrier();
     for (int kt = 0; kt < KT - 2; kt += 2) {
         gload(kt + 2, C0{});
         compute(C0{});
         sstore(C1{}, C1{});
-        __syncthreads();
+        lds_barrier();
         gload(kt + 3, C1{});
         compute(C1{});
         sstore(C0{}, C0{});
-        __syncthreads();
+        lds_barrier();
     }
     compute(C0{});
     sstore(C1{}, C1{});
-    __syncthreads();
+    lds_barrier();
     compute(C1{});
     __syncthreads();  // every wave is done with the LDS stages
 
-    // ---- epilogue -----------------------------------------------------------
-    constexpr int HALF = BM / 2;          // rows staged per pass (one wave-row)
-    constexpr int OTS = BN + 8;           // int32 row stride of the staging tile
-    float* as_l = reinterpret_cast<float*>(smem);
-    float* ws_l = as_l + BM;
-    int32_t* ot = reinterpret_cast<int32_t*>(ws_l + BN);
-    for (int t = tid; t < BM; t += NT) {
-        const int mr = m0 + t;
-        float v = 0.f;
-        if (mr < m1) v = as[(GROUPED && row_index != nullptr) ? row_index[mr] : mr];
-        as_l[t] = v;
-    }
-    for (int t = tid; t < BN; t += NT) ws_l[t] = (n0 + t < N) ? wsexp[n0 + t] : 0.f;
-
-#pragma unroll
-    for (int pass = 0; pass < 2; pass++) {
-        if (wm == pass) {
-            // lane l, register r of block (i, j): row 8*(r/4) + 4*(l/32) + r%4, col l%32
-#pragma unroll
-            for (int i = 0; i < FM; i++)
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        const int col = wn * WTN + j * 32 + (lane & 31);
-                        ot[row * OTS + col] = acc[i][j][r];
-                    }
-        }
-        __syncthreads();
-        // stream the staged half: BN/4 chunks of 4 columns per row; a wave covers
-        // whole rows, so the row scale is uniform across the wave
-        constexpr int CHR = BN / 4;
-        for (int c = tid; c < HALF * CHR; c += NT) {
-            const int rl = c / CHR, cl = (c % CHR) * 4;
-            const int row_t = pass * HALF + rl;
-            const int mr = m0 + row_t;
-            const int col = n0 + cl;
-            if (mr >= m1 || col >= N) continue;
-            const i32x4 a4 = *reinterpret_cast<const i32x4*>(ot + rl * OTS + cl);
-            const float asc = as_l[row_t];
-            uint16_t h[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                float v = (float)a4[q] * asc;
-                v = v * ws_l[cl + q];
-                if (bexp != nullptr && col + q < N) v = v + fni8::h2f(bexp[col + q]);
-                h[q] = fni8::f2h(v);
-            }
-            uint16_t* yp = y + (int64_t)mr * ldy + col;
-            if (col + 3 < N && ((uintptr_t)yp & 7) == 0) {
-                uint2 pk;
-                pk.x = h[0] | ((uint32_t)h[1] << 16);
-                pk.y = h[2] | ((uint32_t)h[3] << 16);
-                *reinterpret_cast<uint2*>(yp) = pk;
-            } else {
-                for (int q = 0; q < 4 && col + q < N; q++) yp[q] = h[q];
-            }
-            if constexpr (WRITE_ACC) {
-                for (int q = 0; q < 4 && col + q < N; q++) acc_out[(int64_t)mr * N + col + q] = a4[q];
-            }
-        }
-        __syncthreads();
-    }
+    tile_epilogue<BM, BN, GROUPED, WRITE_ACC>(acc, smem, tid, lane, wm, wn, m0, m1, n0, N,
+                                              row_index, as, wsexp, bexp, y, ldy, acc_out);
 }
 
 template <int BM, int BN, int BK, bool GROUPED>
