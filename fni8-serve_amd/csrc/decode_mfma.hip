@@ -459,7 +459,8 @@ int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, 
 }
 
 // Launch shapes by M tile and weight shape, measured on MI355X over the
-// Qwen3-8B decode linears (36 distinct weight copies, weights from HBM).
+// Qwen3-8B decode linears (a sweep of every shape within the LDS budget, 24
+// distinct weight copies, weights from HBM).
 // Other shapes take the first generic entry whose wave split divides K.
 template <int MT>
 int launch_mt(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const int8_t* w,
@@ -473,17 +474,17 @@ int launch_mt(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, cons
     } while (0)
     const bool wide = N >= 16384, longk = K >= 8192, narrow = N <= 4096;
     if constexpr (MT == 1) {
-        if (wide) FNI8_DM(2, 4, 1);
+        if (wide) FNI8_DM(2, 2, 1);
         else if (longk) FNI8_DM(1, 8, 2);
         else if (narrow) FNI8_DM(1, 4, 2);
-        else FNI8_DM(2, 4, 2);
-    } else if constexpr (MT == 2) {
-        if (wide) FNI8_DM(2, 4, 1);
-        else if (longk || narrow) FNI8_DM(1, 4, 2);
         else FNI8_DM(2, 8, 1);
+    } else if constexpr (MT == 2) {
+        if (wide) FNI8_DM(2, 2, 1);
+        else if (longk || narrow) FNI8_DM(1, 4, 2);
+        else FNI8_DM(2, 4, 2);
     } else {
-        if (wide) FNI8_DM(2, 8, 1);
-        else if (longk) FNI8_DM(1, 4, 1);
+        if (wide) FNI8_DM(2, 2, 1);
+        else if (longk) FNI8_DM(1, 4, 2);
         else if (narrow) FNI8_DM(1, 8, 1);
         else FNI8_DM(2, 8, 1);
     }
