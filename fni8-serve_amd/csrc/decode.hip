@@ -262,10 +262,10 @@ int launch_gemv(const void* x, int64_t ldx, const float* xs_in, int M, int K, co
     return FNI8_OK;
 }
 
-// Launch shapes, measured on MI355X over the Qwen3-8B decode shapes (36
-// distinct weight copies, so every byte streams from HBM): 4 waves split K; a
-// wide N takes 32-row workgroups (fewer of them re-quantize the activations),
-// narrow N 16-row ones (enough workgroups to fill 256 CUs).  Shapes the tuned
+// Launch shapes, measured on MI355X over the Qwen3-8B decode shapes (24-36
+// distinct weight copies, so every byte streams from HBM; the one-token entries
+// from a sweep of rows x waves x batch): the waves split K; 8-row workgroups
+// take every shape but the narrow N = 4096, K = 4096 one (16-row).  Shapes the tuned
 // entries do not divide take the first generic entry whose batch size divides
 // the per-wave share of K.
 template <bool FUSED>
@@ -299,10 +299,10 @@ int launch_decode_gemv(const void* x, int64_t ldx, const float* xs_in, int M, in
     if (M <= 1) {
         if (K <= 4096) {
             if (N <= 4096) FNI8_GEMV(1, 2, 4, 8, 2);
-            else if (N <= 8192) FNI8_GEMV(1, 4, 4, 4, 2);
-            else FNI8_GEMV(1, 1, 4, 8, 2);
+            else if (N <= 8192) FNI8_GEMV(1, 1, 4, 4, 2);
+            else FNI8_GEMV(1, 1, 4, 2, 2);
         } else {
-            FNI8_GEMV(1, 2, 4, 8, 6);
+            FNI8_GEMV(1, 1, 8, 4, 3);
         }
         FNI8_GEMV_GENERIC(1);
     }
