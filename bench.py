@@ -257,8 +257,8 @@ def moe_section(pkg, wl, device, ts=(16, 256, 4096)):
             _, _, wd, sd = copies[idx[0] % 2]
             idx[0] += 1
             pkg.gemm_w8a8_grouped(aq, as_, wd, sd, seg, R)
-        t_gu = time_eager(gate_up, reps=6)
-        t_dn = time_eager(down, reps=6)
+        t_gu = min(time_burst(gate_up, reps=12) for _ in range(2))
+        t_dn = min(time_burst(down, reps=12) for _ in range(2))
         b = wl.grouped_bytes(active, R, 2 * I, H) + wl.grouped_bytes(active, R, H, I)
         ops = wl.linear_ops(R, 2 * I, H) + wl.linear_ops(R, H, I)
         t = t_gu + t_dn

@@ -495,9 +495,10 @@ int launch_mt(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, cons
     return 1;
 }
 
-// Grouped (MoE) shapes: 2-wave workgroups over 32 weight rows measured fastest
-// on the 128-expert top-8 routing (gate_up 1536x2048, down 2048x768) at
-// T = 16 and 256, ahead of 4- and 8-wave splits.
+// Grouped (MoE) shapes, from a sweep over the 128-expert top-8 routing
+// (gate_up 1536x2048, down 2048x768) at T = 16, 64 and 256: a short K (down's 6
+// slabs) takes one wave over 32 weight rows; otherwise 2-wave workgroups, over
+// 64 weight rows when the tile holds 32 tokens.
 template <int MT>
 int launch_grouped_mt(const int8_t* xq, int64_t ldx, const float* xs, const int32_t* rmap, int R,
                       int K, const int8_t* w, const float* ws, int E, int N,
@@ -509,6 +510,8 @@ int launch_grouped_mt(const int8_t* xq, int64_t ldx, const float* xs, const int3
                                                     acc_out, st, rmap, E, seg_off);             \
         if (rc != 1) return rc;                                                                 \
     } while (0)
+    if (K <= 1024) FNI8_DG(2, 1, 1);
+    if constexpr (MT == 2) FNI8_DG(4, 2, 1);
     FNI8_DG(2, 2, 1);
     FNI8_DG(1, 2, 1);
     FNI8_DG(2, 1, 1);
