@@ -778,7 +778,7 @@ int launch_error(const char* what) {
 
 constexpr size_t kLdsBytes = 160 * 1024;
 constexpr int64_t kSliceMaxM = 16;  // rows up to which the sliced GEMV beats the tile grid
-constexpr int64_t kMfmaMinM = 4;    // from this many rows on the MFMA decode kernel runs first
+constexpr int64_t kMfmaMinM = 1;    // above this many rows the MFMA decode kernel runs first
 
 // Static LDS of w4a8_gemv_kernel<MT, CPG>: the per-wave group sums.
 template <int MT, int CPG>
@@ -1031,6 +1031,11 @@ int launch_linear_w4a8_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t 
                              const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
                              float* xs_out, hipStream_t st) {
     if (M == 0) return FNI8_OK;
+    // One token: the streaming kernel with the quantization fused.  From two
+    // tokens on, a quantize launch plus the MFMA decode kernel is faster than
+    // the VALU-bound stream kernel (Qwen3-8B shapes at 4 tokens: 9.7 / 8.0 /
+    // 17.7 / 16.0 us against 12.0 / 9.2 / 26.9 / 20.9 us).
+    if (M > 1 && G >= 64 && K % 256 == 0) return 1;
     return stream_dispatch<true>(x, ldx, nullptr, M, K, w, ws, N, G, bias, y, ldy, xq_out,
                                  xs_out, st);
 }
