@@ -83,6 +83,76 @@ __global__ __launch_bounds__(kSortThreads) void moe_sort_kernel(
     }
 }
 
+// Combine for k <= KM (the common top-8): the slots are sorted by expert id
+// with an odd-even transposition network (static register indices, stable, so
+// the order is that of the insertion sort below), all k rows of the token are
+// loaded up front, then summed in that order with the same fp16 roundings.
+template <int KM>
+__global__ __launch_bounds__(256) void moe_combine_small_kernel(
+    const uint16_t* __restrict__ yr, int H, const int32_t* __restrict__ topi,
+    const uint16_t* __restrict__ topw, const int32_t* __restrict__ pos, int k,
+    int Tk, uint16_t* __restrict__ out) {
+    const int t = blockIdx.x;
+    int eid[KM], ord[KM];
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+        eid[j] = j < k ? topi[(int64_t)t * k + j] : 0x7fffffff;
+        ord[j] = j;
+    }
+#pragma unroll
+    for (int r = 0; r < KM; r++)
+#pragma unroll
+        for (int a = r & 1; a + 1 < KM; a += 2)
+            if (eid[a] > eid[a + 1]) {
+                const int e0 = eid[a], o0 = ord[a];
+                eid[a] = eid[a + 1];
+                ord[a] = ord[a + 1];
+                eid[a + 1] = e0;
+                ord[a + 1] = o0;
+            }
+    int64_t row[KM];
+    float wgt[KM];
+    bool ok[KM];
+#pragma unroll
+    for (int j = 0; j < KM; j++) {
+        ok[j] = false;
+        row[j] = 0;
+        wgt[j] = 0.f;
+        if (j < k) {
+            const int slot = ord[j];
+            row[j] = pos[(int64_t)t * k + slot];
+            wgt[j] = fni8::h2f(topw[(int64_t)t * k + slot]);
+            ok[j] = row[j] >= 0 && row[j] < Tk;
+        }
+    }
+    for (int h0 = threadIdx.x * 8; h0 < H; h0 += 256 * 8) {
+        uint4 v[KM];
+#pragma unroll
+        for (int j = 0; j < KM; j++)
+            v[j] = ok[j] ? *reinterpret_cast<const uint4*>(yr + row[j] * H + h0) : make_uint4(0, 0, 0, 0);
+        uint16_t ob[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) ob[i] = 0;
+#pragma unroll
+        for (int j = 0; j < KM; j++) {
+            if (!ok[j]) continue;
+            const uint32_t w4[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const uint16_t c = (uint16_t)(w4[i >> 1] >> ((i & 1) * 16));
+                const uint16_t pr = fni8::f2h(fni8::h2f(c) * wgt[j]);
+                ob[i] = fni8::f2h(fni8::h2f(ob[i]) + fni8::h2f(pr));
+            }
+        }
+        uint4 st;
+        st.x = ob[0] | ((uint32_t)ob[1] << 16);
+        st.y = ob[2] | ((uint32_t)ob[3] << 16);
+        st.z = ob[4] | ((uint32_t)ob[5] << 16);
+        st.w = ob[6] | ((uint32_t)ob[7] << 16);
+        *reinterpret_cast<uint4*>(out + (int64_t)t * H + h0) = st;
+    }
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const uint16_t* __restrict__ yr, int H, const int32_t* __restrict__ topi,
@@ -169,7 +239,10 @@ int launch_moe_combine(const uint16_t* yr, int64_t H, const int32_t* topi,
                        uint16_t* out, hipStream_t st) {
     if (T == 0) return FNI8_OK;
     const bool vec = (H % 8 == 0) && ((uintptr_t)yr % 16 == 0) && ((uintptr_t)out % 16 == 0);
-    if (vec)
+    if (vec && k <= 8)
+        hipLaunchKernelGGL(moe_combine_small_kernel<8>, dim3((unsigned)T), dim3(256), 0, st, yr,
+                           (int)H, topi, topw, pos, (int)k, (int)(T * k), out);
+    else if (vec)
         hipLaunchKernelGGL(moe_combine_kernel<true>, dim3((unsigned)T), dim3(256), 0, st, yr,
                            (int)H, topi, topw, pos, (int)k, (int)(T * k), out);
     else

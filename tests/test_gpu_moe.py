@@ -173,3 +173,44 @@ def test_sparse_moe_close_to_cpu_reference(pkg, wl, cuda):
     rel = np.linalg.norm(out - ref) / np.linalg.norm(ref)
     print(f"grouped MoE vs CPU loop: cos {cos:.6f}, relative error {rel:.2e}", flush=True)
     assert cos > 0.999 and rel < 2e-2
+
+
+@pytest.mark.parametrize("k", [1, 3, 8, 12])
+@pytest.mark.parametrize("H", [2048, 204])
+def test_combine_topk_widths(pkg, cuda, k, H):
+    """The top-8 combine (k <= 8 and H % 8 == 0: slots ordered by a sorting
+    network, every row of the token loaded before the sum) and the generic one
+    (k > 8, or H not a multiple of 8) against the oracle, bit for bit."""
+    E, T = 64, 37
+    rng = np.random.default_rng(k * 1000 + H)
+    topi = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    topw = rng.random((T, k)).astype(np.float16)
+    y = rng.standard_normal((T * k, H)).astype(np.float16)
+    _, _, pos = pkg.moe_sort(torch.from_numpy(topi).cuda(), E)
+    out = pkg.moe_combine(torch.from_numpy(y).cuda(), torch.from_numpy(topi).cuda(),
+                          torch.from_numpy(topw).cuda(), pos)
+    _, _, _, pos_r = oracle.moe_sort(topi, E)
+    out_r = oracle.moe_combine_f16(y, topi, topw, pos_r)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), out_r.view(np.uint16))
+
+
+@pytest.mark.parametrize("k", [4, 8])
+def test_combine_skips_out_of_range_experts(pkg, cuda, k):
+    """A slot whose expert id is out of range has no row (the sort marks it -1):
+    the combine leaves it out of the sum.  The oracle gets the same slots with
+    weight 0 on row 0, which adds +0 to a finite sum."""
+    E, T, H = 16, 9, 512
+    rng = np.random.default_rng(k)
+    topi = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    topi[0, 0], topi[3, k - 1], topi[5, 1] = E + 3, -1, E
+    topw = (rng.random((T, k)) + 0.1).astype(np.float16)
+    y = rng.standard_normal((T * k, H)).astype(np.float16)
+    _, _, pos = pkg.moe_sort(torch.from_numpy(topi).cuda(), E)
+    out = pkg.moe_combine(torch.from_numpy(y).cuda(), torch.from_numpy(topi).cuda(),
+                          torch.from_numpy(topw).cuda(), pos)
+    pos_h = pos.cpu().numpy()
+    bad = (topi < 0) | (topi >= E)
+    assert (pos_h[bad] == -1).all() and (pos_h[~bad] >= 0).all()
+    out_r = oracle.moe_combine_f16(y, topi, np.where(bad, np.float16(0), topw),
+                                   np.where(bad, 0, pos_h).astype(np.int32))
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), out_r.view(np.uint16))
