@@ -167,3 +167,15 @@ def test_w4a8_mfma_strided_rows(pkg):
     big = _x(M, K + 256, seed=6)
     x = big[:, 128:128 + K]
     _check(pkg, x, qt, None)
+
+
+@pytest.mark.parametrize("N", [1, 8, 17])
+@pytest.mark.parametrize("M", [2, 9, 40])
+def test_w4a8_mfma_decode_narrow_n(pkg, M, N):
+    """Fewer weight rows than one 16-row block (rows past N repeat row N-1 and
+    are never stored), and one row past a block."""
+    print(f"w4a8 mfma narrow M={M} N={N}", flush=True)
+    K, G = 512, 64
+    qt = _w4(pkg, N, K, G, seed=M + N)
+    bias = torch.randn(N, device="cuda").half()
+    _check(pkg, _x(M, K, seed=M * 3 + N), qt, bias)
