@@ -184,7 +184,7 @@ class FQReader:
                 raise ValueError(f"{path}: not a .fni8 container (bad magic)")
             version = struct.unpack_from("<I", self._mm, 8)[0]
             if version != FORMAT_VERSION:
-                raise ValueError(f"{path}: container version {version}, this build reads "
+                raise ValueError(f"{path}: container version {version}, this library reads "
                                  f"{FORMAT_VERSION}")
             hoff, hlen, tail = _TRAILER.unpack_from(self._mm, size - _TRAILER.size)
             if tail != MAGIC or hoff + hlen != size - _TRAILER.size or hoff < 16:

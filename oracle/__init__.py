@@ -1,7 +1,7 @@
 """CPU oracle for the W8A8 linear path (test infrastructure only).
 
 Only `tests/`, `__graft_entry__.smoke()` and the CPU-baseline leg of `bench.py`
-may import this package, and only as the checker or the timed CPU baseline.
+may import this package, and only to check results or as the timed CPU baseline.
 The product path (the `fni8serve_amd` package) never imports it.
 """
 from .oracle import (  # noqa: F401

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the producers of the linears' fp16 inputs: act_and_mul and
  * RMSNorm, alone and followed by the per-token quantization.  TEST
- * INFRASTRUCTURE ONLY: the checker the HIP kernels are compared against.
+ * INFRASTRUCTURE ONLY: the CPU restatement the HIP kernels are compared against.
  *
  * What it restates (reference = Josephur/fni8-serve):
  *   - act_and_mul: out = act(gate) * up over a merged [.., 2I] row, first half

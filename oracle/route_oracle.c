@@ -1,6 +1,6 @@
 /*
- * CPU oracle for the MoE router.  TEST INFRASTRUCTURE ONLY: the checker the
- * HIP routing kernel is compared against.
+ * CPU oracle for the MoE router.  TEST INFRASTRUCTURE ONLY: the CPU
+ * restatement the HIP routing kernel is compared against.
  *
  * Restates the routing of SparseMoE.forward (reference
  * fni8serve/models/moe.py:62-97), evaluated in fp32 with one rounding per

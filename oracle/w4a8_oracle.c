@@ -1,6 +1,6 @@
 /*
  * CPU oracle for the W4A8 linear (per_group_i4 int4 weights).  TEST
- * INFRASTRUCTURE ONLY: the checker the HIP kernels are compared against.
+ * INFRASTRUCTURE ONLY: the CPU restatement the HIP kernels are compared against.
  *
  * What it restates (reference = Josephur/fni8-serve):
  *   - the weight format of per_group_i4 (fni8serve/convert.py:69-79, unpacked
@@ -8,7 +8,7 @@
  *     byte k/2, low nibble for even k and high nibble for odd k, a nibble u
  *     meaning u - 16 when u >= 8; fp32 scale [N, K/G] per group of G codes;
  *   - `gemm_w4a8`, the int4 GEMM of `fni8.linear` (linear.py:9), whose closed
- *     arithmetic is replaced by this build's convention: per group the exact
+ *     arithmetic is replaced by this library's convention: per group the exact
  *     int32 sum acc_g = sum of xq[m, k] * code[n, k]; accf = fmaf(acc_g,
  *     ws[n, g], accf) over g = 0, 1, ... from +0; y = fp16(accf * xs[m]
  *     (+ bias[n])), one rounding per operation;
