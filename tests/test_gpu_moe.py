@@ -87,6 +87,10 @@ def test_grouped_gemm_bitexact(pkg, wl, cuda, T, proj):
     ([0, 1, 5, 0, 3, 2, 0, 1], 200, 768),        # ~1.5 rows/expert: 16-row tiles, 2-wave K split
     ([0, 70, 1, 17, 33, 0, 2, 4], 1536, 2048),   # ~16 rows/expert: 32-row tiles, a 3-tile segment
     ([40, 0, 64, 65, 1, 30, 48, 63], 104, 1024),  # ~39 rows/expert: 32-row tiles, N % 32 != 0
+    # > 48 rows/expert: the MFMA tile kernel over 128-row tiles, partial last tiles
+    ([0, 1, 63, 64, 65, 127, 128, 129, 191, 192, 255, 256, 300, 700], 264, 768),
+    ([129, 0, 383, 64, 2, 256], 512, 2048),
+    ([0, 1, 63, 64, 65, 127, 128, 129, 300], 200, 640),  # K % 256 != 0: 64-byte K steps
 ])
 @pytest.mark.parametrize("gather", [False, True])
 def test_grouped_mfma_segments_bitexact(pkg, wl, cuda, sizes, N, K, gather):
