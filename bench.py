@@ -646,9 +646,9 @@ def run_sections(result, sections, pkg, wl, pool, device):
     if "roofline" in sections:
         result["roofline"] = kernel_roofline(pkg, wl, pool, device)
         tr = load_traffic(ROOT)
-        if tr is not None:
+        if tr is not None and "hbm_bytes_per_launch" in tr:
             result["roofline"]["traffic"] = tr["hbm_bytes_per_launch"]
-            result["roofline"]["traffic_source"] = tr["source"]
+            result["roofline"]["traffic_source"] = tr.get("source")
         log(f"roofline: {result['roofline']}")
     if "copycal" in sections:
         result["copy_calibration"] = copy_calibration(device)
