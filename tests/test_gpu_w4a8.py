@@ -179,3 +179,13 @@ def test_w4a8_mfma_decode_narrow_n(pkg, M, N):
     qt = _w4(pkg, N, K, G, seed=M + N)
     bias = torch.randn(N, device="cuda").half()
     _check(pkg, _x(M, K, seed=M * 3 + N), qt, bias)
+
+
+@pytest.mark.parametrize("M,N,K", [(65, 264, 1024), (300, 520, 2048), (512, 1000, 4096)])
+def test_w4a8_tile8_group256_bitexact(pkg, M, N, K):
+    """Group size 256 above 64 tokens: the 8-wave two-stage tile kernel (two
+    workgroup rows, ragged M and N, bias), every element against the oracle."""
+    print(f"w4a8 tile8 M={M} N={N} K={K}", flush=True)
+    qt = _w4(pkg, N, K, 256, seed=M + N)
+    bias = torch.randn(N, device="cuda").half()
+    _check(pkg, _x(M, K, seed=M * 7 + K), qt, bias)
