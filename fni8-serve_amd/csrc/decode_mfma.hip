@@ -60,16 +60,22 @@ __device__ __forceinline__ void lds_barrier() {
 
 // Weight side of one wave: pointers and LDS offsets for the 2*NB load
 // instructions of a slab, and the B-fragment offsets for the MFMA.
-template <int NB>
+// RB = 8-row load groups of the workgroup (at most 2 * NB): a workgroup may own
+// fewer rows than its NB MFMA blocks span, so that the workgroup count fits the
+// CUs (6144 rows in 24-row workgroups are 256 of them); the MFMA reads the
+// unloaded rows of the tile as whatever they hold, and those columns are never
+// stored.
+template <int NB, int RB = 2 * NB>
 struct WeightLanes {
-    const int8_t* src[2 * NB];
-    int woff[2 * NB];
+    static_assert(RB >= 1 && RB <= 2 * NB, "load groups within the MFMA blocks");
+    const int8_t* src[RB];
+    int woff[RB];
     int roff[NB][2];
     __device__ __forceinline__ void init(const int8_t* w, int n0, int N, int64_t K, int s0,
                                          int lane) {
         const int rq = lane >> 3, c = lane & 7, r = lane & 15, g = lane >> 4;
 #pragma unroll
-        for (int h = 0; h < 2 * NB; h++) {
+        for (int h = 0; h < RB; h++) {
             const int row = h * 8 + rq;
             int n = n0 + row;
             n = n < N ? n : N - 1;  // rows past N load real memory, never stored
@@ -87,7 +93,7 @@ struct WeightLanes {
 // lane l, register i holds token mt*16 + 4*(l/16) + i, row b*16 + l%16.
 // Token m of the tile is output row r0 + m; its activation scale is
 // xs[rmap[r0 + m]] (xs[r0 + m] without a row map).
-template <int MT, int NB, int WAVES>
+template <int MT, int NB, int WAVES, int WROWS = 16 * NB>
 __device__ __forceinline__ void reduce_store(i32x4 (&acc)[2][MT][NB], i32x4* red, int wave,
                                              int lane, int tid, int n0, int r0, int M, int N,
                                              const float* xs, const int32_t* __restrict__ rmap,
@@ -107,7 +113,7 @@ __device__ __forceinline__ void reduce_store(i32x4 (&acc)[2][MT][NB], i32x4* red
 #pragma unroll
         for (int wv = 1; wv < WAVES; wv++) s += red[(wv * MT * NB + mb) * 64 + ln];
         const int col = n0 + b * 16 + (ln & 15);
-        if (col >= N) continue;
+        if (b * 16 + (ln & 15) >= WROWS || col >= N) continue;
         const float wsc = ws[col];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -126,7 +132,7 @@ __device__ __forceinline__ void reduce_store(i32x4 (&acc)[2][MT][NB], i32x4* red
 // sorted rows; tile slot blockIdx.x is one 16*MT-row piece of one expert's
 // segment, blockIdx.y the weight-row block; sorted row r reads activation row
 // rmap[r]; weights, scales and bias are stacked per expert).
-template <int MT, int NB, int WAVES, int SB, bool GROUPED>
+template <int MT, int NB, int WAVES, int SB, bool GROUPED, int RB = 2 * NB>
 __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
     const int8_t* __restrict__ xq, int64_t ldx, const float* __restrict__ xs,
     const int32_t* __restrict__ rmap, int M, int K, const int8_t* __restrict__ w,
@@ -148,18 +154,18 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
         int e, r1;
         if (!fni8::find_group_tile(seg_off, E, 16 * MT, blockIdx.x, e, r0, r1)) return;
         M = r1 - r0;
-        n0 = blockIdx.y * ROWS;
+        n0 = blockIdx.y * (8 * RB);
         w += (int64_t)e * N * K;
         ws += (int64_t)e * N;
         if (bias != nullptr) bias += (int64_t)e * N;
     } else {
-        n0 = blockIdx.x * ROWS;
+        n0 = blockIdx.x * (8 * RB);
     }
     const int per = (K >> 7) / WAVES;  // slabs per wave (exact: the launcher checks)
     const int s0 = wave * per, nb = per / SB;
     const int rq = lane >> 3, c = lane & 7, r = lane & 15, g = lane >> 4;
 
-    WeightLanes<NB> wl;
+    WeightLanes<NB, RB> wl;
     wl.init(w, n0, N, K, s0, lane);
     // activation rows: load lane -> (token h*8 + rq, chunk c); tokens past M
     // repeat token M-1 (computed, never stored)
@@ -179,13 +185,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
 #pragma unroll
         for (int q = 0; q < 2; q++) aoff[mt][q] = (ROWS + mt * 16 + r) * 128 + swz(mt * 16 + r, 4 * q + g);
 
-    i32x4 wa[SB][2 * NB], wb[SB][2 * NB];
+    i32x4 wa[SB][RB], wb[SB][RB];
     i32x4 xa[SB][2 * MT], xb[SB][2 * MT];
-    auto load = [&](i32x4 (&dw)[SB][2 * NB], i32x4 (&dx)[SB][2 * MT], int bt) {
+    auto load = [&](i32x4 (&dw)[SB][RB], i32x4 (&dx)[SB][2 * MT], int bt) {
 #pragma unroll
         for (int j = 0; j < SB; j++)
 #pragma unroll
-            for (int h = 0; h < 2 * NB; h++) dw[j][h] = ld16_nt(wl.src[h] + (int64_t)(bt * SB + j) * 128);
+            for (int h = 0; h < RB; h++) dw[j][h] = ld16_nt(wl.src[h] + (int64_t)(bt * SB + j) * 128);
 #pragma unroll
         for (int j = 0; j < SB; j++)
 #pragma unroll
@@ -200,7 +206,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
             for (int b = 0; b < NB; b++) acc[q][mt][b] = i32x4{0, 0, 0, 0};
 
     int8_t* st = smem + wave * (SB * TILE);
-    auto compute = [&](const i32x4 (&wv)[SB][2 * NB], const i32x4 (&xv)[SB][2 * MT]) {
+    auto compute = [&](const i32x4 (&wv)[SB][RB], const i32x4 (&xv)[SB][2 * MT]) {
         // The tile is private to the wave and LDS executes a wave's accesses in
         // order; the barriers only keep the compiler from reordering across them.
         __builtin_amdgcn_wave_barrier();
@@ -208,7 +214,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
 #pragma unroll
         for (int j = 0; j < SB; j++) {
 #pragma unroll
-            for (int h = 0; h < 2 * NB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + wl.woff[h]) = wv[j][h];
+            for (int h = 0; h < RB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + wl.woff[h]) = wv[j][h];
 #pragma unroll
             for (int h = 0; h < 2 * MT; h++) *reinterpret_cast<i32x4*>(st + j * TILE + xwoff[h]) = xv[j][h];
         }
@@ -242,7 +248,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
 #pragma unroll
         for (int j = 0; j < SB; j++) {
 #pragma unroll
-            for (int h = 0; h < 2 * NB; h++) wa[j][h] = wb[j][h];
+            for (int h = 0; h < RB; h++) wa[j][h] = wb[j][h];
 #pragma unroll
             for (int h = 0; h < 2 * MT; h++) xa[j][h] = xb[j][h];
         }
@@ -250,14 +256,14 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
     compute(wa, xa);
 
     __syncthreads();  // the reduction area overlaps the tiles
-    reduce_store<MT, NB, WAVES>(acc, red, wave, lane, tid, n0, r0, M, N, xs,
+    reduce_store<MT, NB, WAVES, 8 * RB>(acc, red, wave, lane, tid, n0, r0, M, N, xs,
                                 GROUPED ? rmap : nullptr, ws, bias, y, ldy, acc_out);
 }
 
 // ---- fp16 activations, M <= 4, quantized in the kernel ----------------------
 // PQ: each wave's K share is 4*PQ slabs (K = 512 * WAVES * PQ exactly), which
 // makes every loop trip count a compile-time constant.
-template <int NB, int WAVES, int SB, int PQ>
+template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB>
 __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int M, int K, const int8_t* __restrict__ w,
     const float* __restrict__ ws, int N, const uint16_t* __restrict__ bias,
@@ -277,7 +283,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * ROWS;
+    const int n0 = blockIdx.x * (8 * RB);
     const int s0 = wave * PER;
     const int r = lane & 15, g = lane >> 4;
 
@@ -295,13 +301,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
             xv[j] = make_uint4(0, 0, 0, 0);
     }
     // 2. first weight batch
-    WeightLanes<NB> wl;
+    WeightLanes<NB, RB> wl;
     wl.init(w, n0, N, K, s0, lane);
-    i32x4 wa[SB][2 * NB], wb[SB][2 * NB];
+    i32x4 wa[SB][RB], wb[SB][RB];
 #pragma unroll
     for (int j = 0; j < SB; j++)
 #pragma unroll
-        for (int h = 0; h < 2 * NB; h++) wa[j][h] = ld16_nt(wl.src[h] + (int64_t)j * 128);
+        for (int h = 0; h < RB; h++) wa[j][h] = ld16_nt(wl.src[h] + (int64_t)j * 128);
 
     // 3. row max magnitudes: integer max over (bits & 0x7fff), one wave-uniform
     //    value per token, then across the waves
@@ -364,13 +370,13 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
 #pragma unroll
         for (int b = 0; b < NB; b++) acc[q][0][b] = i32x4{0, 0, 0, 0};
     int8_t* st = tiles + wave * (SB * TILE);
-    auto compute = [&](const i32x4 (&wv)[SB][2 * NB], int bt) {
+    auto compute = [&](const i32x4 (&wv)[SB][RB], int bt) {
         __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int j = 0; j < SB; j++)
 #pragma unroll
-            for (int h = 0; h < 2 * NB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + wl.woff[h]) = wv[j][h];
+            for (int h = 0; h < RB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + wl.woff[h]) = wv[j][h];
         __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
 #pragma unroll
@@ -396,21 +402,21 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
 #pragma unroll
         for (int j = 0; j < SB; j++)
 #pragma unroll
-            for (int h = 0; h < 2 * NB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)((bt + 1) * SB + j) * 128);
+            for (int h = 0; h < RB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)((bt + 1) * SB + j) * 128);
         compute(wa, bt);
 #pragma unroll
         for (int j = 0; j < SB; j++)
 #pragma unroll
-            for (int h = 0; h < 2 * NB; h++) wa[j][h] = wb[j][h];
+            for (int h = 0; h < RB; h++) wa[j][h] = wb[j][h];
     }
     compute(wa, NBT - 1);
 
     __syncthreads();  // the reduction area overlaps the tiles
-    reduce_store<1, NB, WAVES>(acc, red, wave, lane, tid, n0, 0, M, N, scl, nullptr, ws, bias, y,
-                               ldy, acc_out);
+    reduce_store<1, NB, WAVES, 8 * RB>(acc, red, wave, lane, tid, n0, 0, M, N, scl, nullptr, ws,
+                                       bias, y, ldy, acc_out);
 }
 
-template <int MT, int NB, int WAVES, int SB, bool GROUPED = false>
+template <int MT, int NB, int WAVES, int SB, bool GROUPED = false, int RB = 2 * NB>
 int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const int8_t* w,
            const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
            int32_t* acc_out, hipStream_t st, const int32_t* rmap = nullptr, int E = 0,
@@ -421,14 +427,14 @@ int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const i
     constexpr size_t red = (size_t)WAVES * MT * NB * 64 * 16;
     constexpr size_t lds = tiles > red ? tiles : red;
     static_assert(lds <= 160 * 1024, "decode GEMM LDS budget");
-    auto kern = decode_mfma_kernel<MT, NB, WAVES, SB, GROUPED>;
+    auto kern = decode_mfma_kernel<MT, NB, WAVES, SB, GROUPED, RB>;
     if constexpr (lds > 64 * 1024) {
         static const bool ok = hipFuncSetAttribute((const void*)kern,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    (int)lds) == hipSuccess;
         if (!ok) return 1;
     }
-    const unsigned nblk = (unsigned)((N + 16 * NB - 1) / (16 * NB));
+    const unsigned nblk = (unsigned)((N + 8 * RB - 1) / (8 * RB));
     // grouped: one slot per 16*MT-row piece of a segment; at most
     // ceil(M / (16*MT)) + E of them are non-empty
     const dim3 grid = GROUPED ? dim3((unsigned)((M + 16 * MT - 1) / (16 * MT) + E), nblk) : dim3(nblk);
@@ -437,7 +443,7 @@ int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const i
     return FNI8_OK;
 }
 
-template <int NB, int WAVES, int SB, int PQ>
+template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB>
 int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, const float* ws,
                  int N, const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
                  float* xs_out, int32_t* acc_out, hipStream_t st) {
@@ -448,14 +454,29 @@ int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, 
     constexpr size_t red = (size_t)WAVES * NB * 64 * 16;
     const size_t lds = lds_main > red ? lds_main : red;
     if (lds > 160 * 1024) return 1;
-    auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ>;
+    auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ, RB>;
     static const bool ok = hipFuncSetAttribute((const void*)kern,
                                                hipFuncAttributeMaxDynamicSharedMemorySize,
                                                160 * 1024) == hipSuccess;
     if (!ok) return 1;
-    hipLaunchKernelGGL(kern, dim3((unsigned)((N + 16 * NB - 1) / (16 * NB))), dim3(WAVES * 64), lds,
+    hipLaunchKernelGGL(kern, dim3((unsigned)((N + 8 * RB - 1) / (8 * RB))), dim3(WAVES * 64), lds,
                        st, x, ldx, M, K, w, ws, N, bias, y, ldy, xq_out, xs_out, acc_out);
     return FNI8_OK;
+}
+
+// True when 24-row workgroups fill the CUs better than 32-row ones in whole
+// rounds (N = 6144: 256 workgroups against 192 on 256 CUs).
+bool prefer_24_rows(int N) {
+    static const int cus = [] {
+        int dev = 0, n = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            n <= 0)
+            n = 256;
+        return n;
+    }();
+    auto fill = [](int wgs) { return (double)wgs / (double)(((wgs + cus - 1) / cus) * cus); };
+    return fill((N + 23) / 24) > fill((N + 31) / 32) + 1e-9;
 }
 
 // Launch shapes by M tile and weight shape, measured on MI355X over the
@@ -466,32 +487,38 @@ template <int MT>
 int launch_mt(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const int8_t* w,
               const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
               int32_t* acc_out, hipStream_t st) {
-#define FNI8_DM(NB, WV, SB)                                                                    \
+#define FNI8_DM_RB(NB, WV, SB, RB)                                                             \
     do {                                                                                       \
-        const int rc = launch<MT, NB, WV, SB>(xq, ldx, xs, M, K, w, ws, N, bias, y, ldy,       \
-                                              acc_out, st);                                    \
+        const int rc = launch<MT, NB, WV, SB, false, RB>(xq, ldx, xs, M, K, w, ws, N, bias, y, \
+                                                         ldy, acc_out, st);                    \
         if (rc != 1) return rc;                                                                \
     } while (0)
+#define FNI8_DM(NB, WV, SB) FNI8_DM_RB(NB, WV, SB, 2 * NB)
     const bool wide = N >= 16384, longk = K >= 8192, narrow = N <= 4096;
+    const bool rows24 = !wide && !narrow && prefer_24_rows(N);  // QKV: 24-row workgroups
     if constexpr (MT == 1) {
         if (wide) FNI8_DM(2, 2, 1);
         else if (longk) FNI8_DM(1, 8, 2);
         else if (narrow) FNI8_DM(1, 4, 2);
+        else if (rows24) FNI8_DM_RB(2, 8, 1, 3);
         else FNI8_DM(2, 8, 1);
     } else if constexpr (MT == 2) {
         if (wide) FNI8_DM(2, 2, 1);
         else if (longk || narrow) FNI8_DM(1, 4, 2);
+        else if (rows24) FNI8_DM_RB(2, 4, 2, 3);
         else FNI8_DM(2, 4, 2);
     } else {
         if (wide) FNI8_DM(2, 2, 1);
         else if (longk) FNI8_DM(1, 4, 2);
         else if (narrow) FNI8_DM(1, 8, 1);
+        else if (rows24) FNI8_DM_RB(2, 8, 1, 3);
         else FNI8_DM(2, 8, 1);
     }
     FNI8_DM(1, 4, 1);
     FNI8_DM(1, 2, 1);
     FNI8_DM(1, 1, 1);
 #undef FNI8_DM
+#undef FNI8_DM_RB
     return 1;
 }
 
@@ -523,12 +550,13 @@ int launch_grouped_mt(const int8_t* xq, int64_t ldx, const float* xs, const int3
 int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w,
                        const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
                        int8_t* xq_out, float* xs_out, int32_t* acc_out, hipStream_t st) {
-#define FNI8_DF(NB, WV, SB, PQ)                                                                 \
+#define FNI8_DF_RB(NB, WV, SB, PQ, RB)                                                          \
     do {                                                                                        \
-        const int rc = launch_fused<NB, WV, SB, PQ>(x, ldx, M, K, w, ws, N, bias, y, ldy,       \
-                                                    xq_out, xs_out, acc_out, st);               \
+        const int rc = launch_fused<NB, WV, SB, PQ, RB>(x, ldx, M, K, w, ws, N, bias, y, ldy,   \
+                                                        xq_out, xs_out, acc_out, st);           \
         if (rc != 1) return rc;                                                                 \
     } while (0)
+#define FNI8_DF(NB, WV, SB, PQ) FNI8_DF_RB(NB, WV, SB, PQ, 2 * NB)
     const bool wide = N >= 16384, narrow = N <= 4096;
     if (wide) {
         FNI8_DF(2, 4, 2, 2);
@@ -537,6 +565,7 @@ int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_
         FNI8_DF(1, 4, 4, 2);
         FNI8_DF(1, 8, 3, 3);
     } else {
+        if (prefer_24_rows(N)) FNI8_DF_RB(2, 8, 2, 1, 3);  // QKV: 24-row workgroups
         FNI8_DF(2, 8, 1, 1);
         FNI8_DF(2, 8, 1, 3);
     }
@@ -550,6 +579,7 @@ int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_
     FNI8_DF(1, 8, 2, 2);
     FNI8_DF(1, 8, 1, 3);
 #undef FNI8_DF
+#undef FNI8_DF_RB
     return 1;
 }
 

@@ -212,3 +212,18 @@ def test_mfma_decode_bias_and_stride(pkg, wl, cuda):
     q, s = wl.weight_i8(N, K, seed=92)
     bias = (torch.randn(N, generator=torch.Generator().manual_seed(93)) * 2).half()
     _linear_full(pkg, x, q, s, bias=bias, tag="mfma bias+stride M=20")
+
+
+@pytest.mark.parametrize("M", [3, 4, 16, 32, 64])
+@pytest.mark.parametrize("N", [5000, 6150])
+def test_24_row_workgroups_ragged_bitexact(pkg, wl, cuda, M, N):
+    """Mid-width linears whose workgroup count fits the CUs better in 24-row
+    workgroups (three 8-row load groups over two 16-row MFMA blocks; the last
+    workgroup holds a partial load group), through the fused kernel (3-4 rows)
+    and the MFMA decode GEMM (more rows), with bias; every element against the
+    oracle."""
+    K = 4096
+    x = wl.activations(M, K, seed=M * 29 + N)
+    q, s = wl.weight_i8(N, K, seed=N + M)
+    bias = torch.from_numpy((np.random.default_rng(N + M).standard_normal(N) * 2).astype(np.float16))
+    _linear_full(pkg, x, q, s, bias=bias, tag=f"24-row M={M} N={N}")
