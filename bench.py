@@ -33,6 +33,7 @@ Also reported (same JSON line):
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -51,6 +52,26 @@ INT8_PEAK_TOPS = 5000.0
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def device_clock_mhz():
+    """Peak shader clock of the current device in MHz (hipDeviceGetAttribute,
+    hipDeviceAttributeClockRate = 5, reported in kHz), or None when the HIP
+    runtime does not answer with a plausible value."""
+    try:
+        # the runtime torch already mapped, so no second HIP runtime is loaded
+        with open("/proc/self/maps") as f:
+            paths = [ln.split()[-1] for ln in f if "libamdhip64.so" in ln]
+        if not paths:
+            return None
+        lib = ctypes.CDLL(paths[0])
+        v = ctypes.c_int()
+        if (lib.hipDeviceGetAttribute(ctypes.byref(v), 5, torch.cuda.current_device()) == 0
+                and 100_000 < v.value < 10_000_000):
+            return v.value / 1000
+    except (OSError, RuntimeError, AttributeError):
+        pass
+    return None
 
 
 def build_pool(wl, pkg, layers, device):
@@ -636,6 +657,7 @@ def main():
                    "step_int8_ops": step_ops, "x": "fp16 N(0,1), 1% outliers x20",
                    "pct_hbm_peak": round(value / HBM_PEAK_GBS * 100, 2),
                    "decode_TOPS": round(step_ops / (ms_per_step * 1e-3) / 1e12, 2),
+                   "peak_sclk_mhz": device_clock_mhz(),
                    "per_M": per_m},
     }
     run_sections(result, sections, pkg, wl, pool, device)
