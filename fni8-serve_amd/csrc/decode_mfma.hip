@@ -508,7 +508,10 @@ int launch_mt(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, cons
         else if (rows24) FNI8_DM_RB(2, 4, 2, 3);
         else FNI8_DM(2, 4, 2);
     } else {
-        if (wide) FNI8_DM(2, 2, 1);
+        // wide at 33..64 tokens: 48-row workgroups (three MFMA blocks) read the
+        // activation tile once per 48 weight rows instead of 32 (gate_up at 64
+        // tokens: 27.3 -> 26.0 us; even at 48 tokens, slower below)
+        if (wide) FNI8_DM_RB(3, 2, 1, 6);
         else if (longk) FNI8_DM(1, 4, 2);
         else if (narrow) FNI8_DM(1, 8, 1);
         else if (rows24) FNI8_DM_RB(2, 8, 1, 3);

@@ -227,3 +227,17 @@ def test_24_row_workgroups_ragged_bitexact(pkg, wl, cuda, M, N):
     q, s = wl.weight_i8(N, K, seed=N + M)
     bias = torch.from_numpy((np.random.default_rng(N + M).standard_normal(N) * 2).astype(np.float16))
     _linear_full(pkg, x, q, s, bias=bias, tag=f"24-row M={M} N={N}")
+
+
+@pytest.mark.parametrize("M", [33, 64])
+@pytest.mark.parametrize("N", [16400, 16431])
+def test_48_row_workgroups_ragged_bitexact(pkg, wl, cuda, M, N):
+    """Wide linears at 33..64 rows run 48-row workgroups (three 16-row MFMA
+    blocks, six 8-row load groups).  N = 16400 leaves the last workgroup a
+    whole MFMA block past N, N = 16431 a partial load group; every element
+    against the oracle, with bias."""
+    K = 4096
+    x = wl.activations(M, K, seed=M * 31 + N)
+    q, s = wl.weight_i8(N, K, seed=N + 2 * M)
+    bias = torch.from_numpy((np.random.default_rng(N - M).standard_normal(N) * 2).astype(np.float16))
+    _linear_full(pkg, x, q, s, bias=bias, tag=f"48-row M={M} N={N}")
