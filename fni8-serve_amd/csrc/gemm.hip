@@ -463,10 +463,10 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
         if (grouped) launch_generic<true>(a, st); else launch_generic<false>(a, st);
     } else if (grouped) {
         // Expert segments: average rows per expert picks the kernel -- the MFMA
-        // decode kernel in grouped form for small segments (the skinny kernel
-        // where it does not take the shape), the tile kernel for large ones.
+        // decode kernel in grouped form up to 4 rows per expert (the skinny
+        // kernel where it does not take the shape), the tile kernel above.
         const double avg = (double)M / (double)E;
-        if (avg <= 48.0) {
+        if (avg <= 4.0) {
             rc = launch_decode_mfma_grouped(aq, lda, as, row_index, M, K, w, ws, E, N, seg_off,
                                             bias, y, ldy, acc_out, st);
             if (rc == 1) {

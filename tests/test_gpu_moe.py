@@ -83,11 +83,18 @@ def test_grouped_gemm_bitexact(pkg, wl, cuda, T, proj):
         assert np.array_equal(y.cpu().numpy()[rows].view(np.uint16), ys.view(np.uint16))
 
 
+_SPARSE = [0, 1, 0, 0, 33, 0, 2, 0, 0, 0, 0, 17, 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0]
+
+
 @pytest.mark.parametrize("sizes,N,K", [
-    ([0, 1, 5, 0, 3, 2, 0, 1], 200, 768),        # ~1.5 rows/expert: 16-row tiles, 2-wave K split
-    ([0, 70, 1, 17, 33, 0, 2, 4], 1536, 2048),   # ~16 rows/expert: 32-row tiles, a 3-tile segment
-    ([40, 0, 64, 65, 1, 30, 48, 63], 104, 1024),  # ~39 rows/expert: 32-row tiles, N % 32 != 0
-    # > 48 rows/expert: the MFMA tile kernel over 128-row tiles, partial last tiles
+    # <= 4 rows/expert: the grouped MFMA decode kernel over 16-row tiles
+    ([0, 1, 5, 0, 3, 2, 0, 1], 200, 768),        # ~1.5 rows/expert, one wave (short K)
+    (_SPARSE, 200, 1024),                        # 2.25 rows/expert, a 3-tile segment
+    (_SPARSE, 136, 2048),                        # the same with 2-wave workgroups
+    # <= 40 rows/expert: the tile kernel over 64-row segment tiles
+    ([0, 70, 1, 17, 33, 0, 2, 4], 1536, 2048),   # ~16 rows/expert, a 2-tile segment
+    ([40, 0, 64, 65, 1, 30, 48, 63], 104, 1024),  # ~39 rows/expert, N % 128 != 0
+    # > 40 rows/expert: the tile kernel over 128-row tiles, partial last tiles
     ([0, 1, 63, 64, 65, 127, 128, 129, 191, 192, 255, 256, 300, 700], 264, 768),
     ([129, 0, 383, 64, 2, 256], 512, 2048),
     ([0, 1, 63, 64, 65, 127, 128, 129, 300], 200, 640),  # K % 256 != 0: 64-byte K steps
