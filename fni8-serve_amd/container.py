@@ -108,7 +108,7 @@ class FQWriter:
         if pad:
             self._f.write(b"\0" * pad)
             self._pos += pad
-        raw = t.view(torch.uint8).reshape(-1).numpy() if t.numel() else b""
+        raw = t.reshape(-1).view(torch.uint8).numpy() if t.numel() else b""
         self._f.write(memoryview(raw))
         entry = {"dtype": _NAMES[t.dtype], "shape": list(t.shape), "offset": self._pos,
                  "nbytes": t.numel() * t.element_size()}

@@ -183,9 +183,12 @@ __device__ __forceinline__ int wave_incl_scan_i32(int v, int lane) {
 // `bm` rows; tile `slot` (counted over all experts in order) is located by one
 // wave with a running prefix over chunks of 64 experts.  Returns false when
 // `slot` is past the last tile.  Every lane of the wave gets the same answer.
+// Rows are bounded by `rows` (the caller's allocation): a tile starting at or
+// beyond it is dropped and r1 is clamped to it, so a seg_off whose last entry
+// exceeds the buffers loses rows instead of reading or writing past them.
 __device__ __forceinline__ bool find_group_tile(const int32_t* __restrict__ seg_off, int E,
-                                                int bm, int slot, int& e_out, int& r0,
-                                                int& r1) {
+                                                int bm, int slot, int rows, int& e_out,
+                                                int& r0, int& r1) {
     const int lane = threadIdx.x & 63;
     int base = 0;
     for (int c = 0; c < E; c += 64) {
@@ -209,7 +212,8 @@ __device__ __forceinline__ bool find_group_tile(const int32_t* __restrict__ seg_
             e_out = eo;
             r0 = lo_s + (slot - base - ex_s) * bm;
             r1 = r0 + bm < hi_s ? r0 + bm : hi_s;
-            return true;
+            r1 = r1 < rows ? r1 : rows;
+            return r0 >= 0 && r0 < r1;
         }
         base += __shfl(incl, 63, 64);
     }

@@ -152,7 +152,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
         // every wave finds the same tile; past the last tile the whole
         // workgroup leaves before any barrier
         int e, r1;
-        if (!fni8::find_group_tile(seg_off, E, 16 * MT, blockIdx.x, e, r0, r1)) return;
+        if (!fni8::find_group_tile(seg_off, E, 16 * MT, blockIdx.x, M, e, r0, r1)) return;
         M = r1 - r0;
         n0 = blockIdx.y * (8 * RB);
         w += (int64_t)e * N * K;

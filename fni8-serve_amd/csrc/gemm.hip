@@ -69,7 +69,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(
     const uint16_t* bexp = bias;
     if constexpr (GROUPED) {
         int e;
-        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, e, m0, m1)) return;
+        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, M, e, m0, m1)) return;
         wexp += (int64_t)e * N * K;
         wsexp += (int64_t)e * N;
         if (bias) bexp += (int64_t)e * N;
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(WAVES_M * WAVES_N * 64) void gemm_tile_kernel(
     if constexpr (GROUPED) {  // x = segment tile slot, y = n-tile
         n0 = blockIdx.y * BN;
         int e;
-        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, e, m0, m1)) return;
+        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, M, e, m0, m1)) return;
         wexp += (int64_t)e * N * K;
         wsexp += (int64_t)e * N;
         if (bias) bexp += (int64_t)e * N;

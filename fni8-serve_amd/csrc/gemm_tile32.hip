@@ -164,7 +164,7 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
     if constexpr (GROUPED) {  // x = segment tile slot, y = n-tile
         n0 = blockIdx.y * BN;
         int e;
-        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, e, m0, m1)) return;
+        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, M, e, m0, m1)) return;
         wexp += (int64_t)e * N * K;
         wsexp += (int64_t)e * N;
         if (bias) bexp += (int64_t)e * N;
@@ -285,9 +285,12 @@ int launch(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_in
     static_assert(lds <= 160 * 1024, "LDS budget");
     const unsigned ntn = (unsigned)((N + BN - 1) / BN);
     dim3 grid = GROUPED ? dim3(slots, ntn) : dim3(ntn * (unsigned)((M + BM - 1) / BM));
-    auto run = [&](auto kern) -> int {
-        // The LDS limit is a per-function attribute; setting it again with the
-        // same value is idempotent, so a race between threads is harmless.
+    // The LDS limit is a per-function attribute, so each instantiation (with and
+    // without the accumulator output) is set once, by its own flag; setting it
+    // again with the same value is idempotent, so a race between threads is harmless.
+    auto run = [&](auto acc_c) -> int {
+        constexpr bool ACC = decltype(acc_c)::value;
+        const auto kern = gemm_tile32_kernel<BM, BN, BK, GROUPED, ACC>;
         static bool attr_set = false;
         if (!attr_set) {
             hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -302,8 +305,8 @@ int launch(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_in
                            E, seg_off, bias, y, ldy, acc_out);
         return FNI8_OK;
     };
-    if (acc_out) return run(gemm_tile32_kernel<BM, BN, BK, GROUPED, true>);
-    return run(gemm_tile32_kernel<BM, BN, BK, GROUPED, false>);
+    if (acc_out) return run(std::true_type{});
+    return run(std::false_type{});
 }
 
 }  // namespace

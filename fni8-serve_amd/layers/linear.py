@@ -71,6 +71,9 @@ class LinearW8A8(nn.Module):
         qt = self.weight
         return qt.scheme == "per_row_i8" or (qt.scheme == "per_group_i4" and qt.codebook == "int4")
 
+    # the reference's name for the same rule (linear.py:58)
+    _dp4a_ok = _int8_ok
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self._int8_ok(x):
             return ops.linear(x, self.weight, bias=self.bias)

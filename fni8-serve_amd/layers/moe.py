@@ -3,7 +3,7 @@
 Same constructor and routing as fni8serve/models/moe.py:25-113 (softmax or
 sigmoid scoring, optional group-limited top-k, renormalisation, routed
 scaling, optional shared expert).  The reference then loops over experts in
-Python, with two host syncs per expert (moe.py:218-224); its docstring names
+Python, with two host syncs per expert (moe.py:99-105); its docstring names
 the grouped GEMM as the intended kernel (moe.py:9-11), and its graph runner
 declines MoE layers for that reason (engine/cuda_graph.py:190-191).  On the
 GPU this module runs instead, with no host sync, so a whole MoE layer can be
@@ -146,7 +146,7 @@ class SparseMoE(nn.Module):
         return ops.moe_combine(y, topi, topw, pos)
 
     def _experts_loop(self, xf: torch.Tensor, topw: torch.Tensor, topi: torch.Tensor):
-        """The reference's per-expert loop (moe.py:216-224), for CPU inputs."""
+        """The reference's per-expert loop (moe.py:97-105), for CPU inputs."""
         out = torch.zeros_like(xf)
         for e in range(self.num_experts):
             mask = topi == e

@@ -3,8 +3,10 @@
 Same constructor and forward contract: `RMSNorm(dim, eps=1e-6, weight=None, *,
 add_unit_offset=False)`; `forward(x, residual=None)` returns the normed tensor,
 or `(normed, x + residual)` with a residual (the fused residual add).  A GPU
-fp16 tensor takes the kernel (`ops.rmsnorm`, one launch); CPU tensors take the
-reference's eager fp32 form (norm.py:37-43, :56-58).  `forward_quant` is the
+fp16 tensor with an fp16 weight takes the kernel (`ops.rmsnorm`, one launch);
+every other input (CPU, or another dtype on the GPU) takes the reference's eager
+fp32 form (norm.py:37-43, :56-58), so no input raises where the reference
+returns a result.  `forward_quant` is the
 fused form for a norm that feeds a W8A8 linear (QKV, gate_up): it returns the
 linear's int8 input and per-token scales instead of the fp16 row.
 """
@@ -35,7 +37,7 @@ class RMSNorm(nn.Module):
         return (xf * w).to(dt)
 
     def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None):
-        if x.is_cuda:
+        if x.is_cuda and x.dtype == torch.float16 and self.weight.dtype == torch.float16:
             return ops.rmsnorm(x, self.weight.detach(), self.eps, residual=residual,
                                unit_offset=self.add_unit_offset)
         if residual is None:

@@ -6,7 +6,7 @@ GEMMs; distributions follow the measurement plan of the hot path:
   W     int8 uniform in [-127, 127]
   w_s   drawn in fp16 from U(0.001, 0.02), stored fp32 (exact)
   MoE   router logits N(0, 1) + a seeded Zipf-like bias -ln(1 + rank[e]),
-        softmax over all experts, top-8, renormalised (fni8serve/models/moe.py:189-214)
+        softmax over all experts, top-8, renormalised (fni8serve/models/moe.py:70-95)
 Every generator takes an explicit seed and a device; generation on "cpu" is
 bit-reproducible across runs, and the GPU gets copies of the same tensors.
 """
@@ -74,7 +74,7 @@ def router_logits(T: int, E: int, seed: int, device="cpu") -> torch.Tensor:
 
 
 def route(logits: torch.Tensor, top_k: int, dtype=torch.float16):
-    """softmax over all experts -> top-k -> renormalise -> cast (moe.py:189-214)."""
+    """softmax over all experts -> top-k -> renormalise -> cast (moe.py:70-95)."""
     scores = torch.softmax(logits.float(), dim=-1)
     topw, topi = torch.topk(scores, top_k, dim=-1)
     topw = topw / topw.sum(dim=-1, keepdim=True).clamp_min(1e-9)

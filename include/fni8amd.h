@@ -98,7 +98,7 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
 /*
  * Routing sort for the grouped expert GEMM (replaces the per-expert
  * `mask = topi == e; mask.nonzero()` gathers of SparseMoE.forward,
- * fni8serve/models/moe.py:218-222).  A stable counting sort of the T*k
+ * fni8serve/models/moe.py:100-103).  A stable counting sort of the T*k
  * (token, slot) pairs by expert id: inside each expert's segment the rows are
  * in ascending token, then slot, order, as nonzero() returns them.
  *   topi       int32 [T, k] expert ids in [0, E)
@@ -113,7 +113,7 @@ int fni8_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E, int32_t*
 /*
  * Grouped W8A8 GEMM over expert segments: all experts' `gemm_w8a8` calls of
  * one projection in one launch (replaces the expert loop's linears,
- * fni8serve/models/moe.py:223 via layers/mlp.py:39-40; the reference notes
+ * fni8serve/models/moe.py:104 via layers/mlp.py:39-40; the reference notes
  * the kernel as future work at moe.py:9-11).
  *   aq, as     int8 [rows, K] (row stride K) and fp32 [rows]: quantized
  *              activations
@@ -131,7 +131,7 @@ int fni8_gemm_w8a8_grouped(const int8_t* aq, const float* as, const int32_t* row
                            void* y, int32_t* acc_out, void* stream);
 
 /*
- * Weighted combine of expert outputs (replaces moe.py:224's
+ * Weighted combine of expert outputs (replaces moe.py:105's
  * `out.index_add_(0, tok_idx, contrib * topw[tok_idx, slot])` over the
  * expert loop): out[t] = sum over the token's slots, in ascending expert id,
  * of fp16(y_sorted[pos[t, j]] * topw[t, j]), accumulated from +0 in fp16.

@@ -17,7 +17,7 @@ parity pinning (how each function is checked, in tests/test_oracle.py):
   dequant_f16 -- fp64 closed form within one fp16 rounding; transposed scale
       indexing fails the check.
   moe_sort / grouped_w8a8_f16 / moe_combine_f16 -- brute force against the
-      reference's per-expert loop restated with `nonzero` in numpy (moe.py:218-224).
+      reference's per-expert loop restated with `nonzero` in numpy (moe.py:99-105).
   quant_identity_check -- not an oracle function: the exhaustive proof, over
       every fp16 (x, amax) pair, that the division-free quantization of the GPU
       decode kernel reproduces quant_rowwise_f16's division (quant_identity.c).

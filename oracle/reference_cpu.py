@@ -9,7 +9,7 @@ for the reference's own tolerance checks (cosine >= 0.99,
 tests/test_smoke.py:68-80).
 
 `reference_moe_loop` restates SparseMoE.forward's routing and expert loop
-(fni8serve/models/moe.py:181-224, softmax scoring, no shared expert) with each
+(fni8serve/models/moe.py:62-105, softmax scoring, no shared expert) with each
 expert linear computed by the W8A8 oracle, so the grouped path can be checked
 against the loop it replaces.
 """
@@ -36,7 +36,7 @@ def reference_cpu_linear(x: torch.Tensor, q: torch.Tensor, s: torch.Tensor,
 
 def route_softmax_topk(x: torch.Tensor, gate: torch.Tensor, top_k: int,
                        norm_topk_prob: bool = True):
-    """moe.py:184-214 (softmax scoring): fp32 router, softmax over all experts,
+    """moe.py:65-95 (softmax scoring): fp32 router, softmax over all experts,
     top-k, renormalise, cast the weights to the activation dtype."""
     xf = x.reshape(-1, x.shape[-1])
     logits = F.linear(xf.float(), gate.float())
@@ -56,7 +56,7 @@ def silu_and_mul_f16(h: np.ndarray) -> np.ndarray:
 
 def reference_moe_loop(xf: np.ndarray, topi: np.ndarray, topw: np.ndarray,
                        gu_q, gu_s, dn_q, dn_s, act=silu_and_mul_f16) -> np.ndarray:
-    """moe.py:216-224 with W8A8 oracle linears: for each expert e in order,
+    """moe.py:97-105 with W8A8 oracle linears: for each expert e in order,
     gather its (token, slot) rows via nonzero, run gate_up -> act -> down,
     weight by topw and index_add into an fp16 zero tensor."""
     T, H = xf.shape

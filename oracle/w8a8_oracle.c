@@ -19,7 +19,7 @@
  *     fni8serve/models/weights.py:18-25).  Exact integer dot products.
  *   - the dequant epilogue: y = fp16(((float)acc * a_s[m]) * w_s[n] (+ bias[n]))
  *     in fp32, one rounding per operation, no fused multiply-add.
- *   - the MoE expert loop (fni8serve/models/moe.py:216-224): rows routed to an
+ *   - the MoE expert loop (fni8serve/models/moe.py:97-105): rows routed to an
  *     expert are gathered in (token, slot) order, run through the expert, and
  *     combined with `index_add_` in ascending expert order in fp16.
  *
@@ -184,7 +184,7 @@ void oracle_linear_w8a8_f16(const uint16_t* x, int64_t ldx, int64_t M, int64_t K
 
 /* Stable counting sort of the T*k (token, slot) pairs by expert id.  The order
  * inside an expert's segment is ascending token then slot: the order
- * `(topi == e).nonzero()` yields at moe.py:219-222.
+ * `(topi == e).nonzero()` yields at moe.py:100-103.
  * seg_off [E+1]; row_token/row_slot [T*k]; pos [T*k] maps (t, j) -> sorted row. */
 int oracle_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E,
                     int32_t* seg_off, int32_t* row_token, int32_t* row_slot, int32_t* pos) {
@@ -211,7 +211,7 @@ int oracle_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E,
 /* Grouped W8A8 GEMM over expert segments.  Sorted row r of expert e reads
  * activation row a_row = (row_index ? row_index[r] : r) of aq/as, and the
  * expert's weight w[e] int8 [N, K] with scales ws[e] fp32 [N].  This is the
- * per-expert loop of moe.py:218-223 with the per-token quantization hoisted
+ * per-expert loop of moe.py:99-104 with the per-token quantization hoisted
  * (quantization is row-local, so gathering before or after quantizing gives
  * identical int8 rows). */
 void oracle_grouped_w8a8_f16(const int8_t* aq, const float* as, int64_t K,
@@ -238,7 +238,7 @@ void oracle_grouped_w8a8_f16(const int8_t* aq, const float* as, int64_t K,
     }
 }
 
-/* Weighted combine (moe.py:214-224): out[t] starts at +0 (zeros_like), then for
+/* Weighted combine (moe.py:97-105): out[t] starts at +0 (zeros_like), then for
  * the token's experts in ascending expert id, out[t] += fp16(contrib * w) with
  * fp16 rounding after the product and after the add. */
 void oracle_moe_combine_f16(const uint16_t* yr /* [R, H] sorted rows */, int64_t H,

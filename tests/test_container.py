@@ -159,6 +159,19 @@ def test_expert_shard_and_names(tmp_path):
         load_fni8_checkpoint(path, device="cpu", names=["experts.9.down"])
 
 
+def test_zero_dim_raw_tensors_roundtrip(tmp_path):
+    """0-d tensors (an optimizer's step count, a scalar buffer) as the reference's
+    training checkpoint writes them through save_fni8 (loader.py save_training_checkpoint)."""
+    path = str(tmp_path / "m.fni8")
+    ts = {"optimizer.state.0.step": torch.tensor(3.0), "count": torch.tensor(7, dtype=torch.int64),
+          "half": torch.tensor(-1.5, dtype=torch.float16)}
+    save_fni8(path, ts)
+    sd = load_fni8_state_dict(path, device="cpu")
+    for name, t in ts.items():
+        assert sd[name].shape == t.shape and sd[name].dtype == t.dtype
+        assert torch.equal(sd[name], t)
+
+
 def test_state_dict_unwraps_raw(tmp_path):
     path = str(tmp_path / "m.fni8")
     ts = _mixed()

@@ -173,6 +173,28 @@ def test_rmsnorm_full_size_and_special_rows(pkg):
     assert np.array_equal(gq.cpu().numpy(), q) and _same_f32(gs.cpu().numpy(), s)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+def test_rmsnorm_module_other_dtypes_take_eager_form(pkg, dt):
+    """GPU inputs the fp16 kernel does not take (fp32, bf16) return the reference's
+    eager result instead of raising (fni8serve/layers/norm.py:50-58)."""
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(8, 256, generator=g).to(dt)
+    r = torch.randn(8, 256, generator=g).to(dt)
+    w = (torch.rand(256, generator=g) + 0.5).to(dt)
+    n = pkg.RMSNorm(256, eps=1e-6, weight=w.clone())
+    ref = n._norm(x)
+    ref_r = n._norm(x + r)
+    n = n.cuda()
+    got = n(x.cuda())
+    got_r, h = n(x.cuda(), r.cuda())
+    torch.cuda.synchronize()
+    assert got.dtype == dt and got_r.dtype == dt
+    tol = 1e-6 if dt == torch.float32 else 1e-2
+    assert torch.allclose(got.cpu().float(), ref.float(), rtol=tol, atol=tol)
+    assert torch.allclose(got_r.cpu().float(), ref_r.float(), rtol=tol, atol=tol)
+    assert torch.equal(h.cpu(), x + r)
+
+
 def test_rmsnorm_against_torch_fp32(pkg):
     """Against the reference's eager form evaluated by torch on the GPU in fp32
     (norm.py:37-43): within 1 fp16 ulp; max abs / rel error printed."""

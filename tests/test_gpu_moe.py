@@ -1,6 +1,6 @@
 """GPU parity of the grouped (MoE) path: routing sort, grouped W8A8 GEMMs and the
 weighted combine, against the oracle and against the per-expert loop it replaces
-(fni8serve/models/moe.py:216-224)."""
+(fni8serve/models/moe.py:97-105)."""
 import numpy as np
 import pytest
 import torch

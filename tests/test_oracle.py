@@ -268,7 +268,7 @@ def test_moe_sort_matches_nonzero_order():
     seg, rt, rs, pos = oracle.moe_sort(topi, E)
     row = 0
     for e in range(E):
-        tok, slot = np.nonzero(topi == e)      # moe.py:219-222 order
+        tok, slot = np.nonzero(topi == e)      # moe.py:100-103 order
         assert seg[e] == row
         assert rt[row:row + len(tok)].tolist() == tok.tolist()
         assert rs[row:row + len(tok)].tolist() == slot.tolist()
@@ -306,7 +306,7 @@ def test_combine_equals_index_add_loop():
     y = (RNG.standard_normal((T * k, H)) * 4).astype(np.float16)
     out = oracle.moe_combine_f16(y, topi, topw, pos)
     ref = np.zeros((T, H), np.float16)
-    for e in range(E):                               # moe.py:218-224
+    for e in range(E):                               # moe.py:99-105
         tok, slot = np.nonzero(topi == e)
         contrib = y[pos[tok, slot]]
         prod = (contrib.astype(np.float32) * topw[tok, slot].astype(np.float32)[:, None]).astype(np.float16)
