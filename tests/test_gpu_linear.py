@@ -113,6 +113,58 @@ def test_prefill_linear_rows(pkg, wl, cuda, name, M):
     print(f"prefill {name} M={M}: quant full + {len(rows)} GEMM rows bit-exact", flush=True)
 
 
+def _sample_rows(M, seed, n=30):
+    rng = np.random.default_rng(seed)
+    return np.unique(np.concatenate([[0, M - 1], rng.choice(M, min(n, M), replace=False)]))
+
+
+@pytest.mark.parametrize("M", [65, 512, 2048, 4096])
+@pytest.mark.parametrize("name", ["qkv", "o", "gate_up", "down"])
+def test_prefill_shipped_kernel_rows(pkg, wl, cuda, name, M):
+    """`linear()` exactly as shipped: no accumulator output, so the kernel
+    instantiation production and the benchmark run (not the parity-only one that
+    also stores int32 accumulators).  fp16 outputs of sampled rows against the
+    oracle, bit for bit."""
+    N, K = wl.QWEN3_8B_LINEARS[name]
+    x = wl.activations(M, K, seed=300 + M)
+    q, s = wl.weight_i8(N, K, seed=20 + SEEDS[name])
+    qt = pkg.QTensor(q.cuda(), s.cuda(), scheme="per_row_i8")
+    y = pkg.linear(x.cuda(), qt)
+    torch.cuda.synchronize()
+    xqr, xsr = oracle.quant_rowwise_f16(x.numpy())
+    rows = _sample_rows(M, M + N)
+    yr = oracle.dequant_f16(oracle.gemm_i8(xqr[rows], q.numpy()), xsr[rows], s.numpy())
+    assert np.array_equal(_f16bits(y)[rows], yr.view(np.uint16)), f"{name} M={M}: fp16 outputs differ"
+
+
+@pytest.mark.parametrize("name,M", [("o", 1), ("o", 2), ("o", 4), ("qkv", 4), ("o", 16),
+                                    ("down", 16), ("qkv", 64), ("gate_up", 33)])
+def test_decode_shipped_kernel_full(pkg, wl, cuda, name, M):
+    """One decode shape per kernel family (fused GEMV, fused MFMA, quantize + MFMA
+    decode GEMM) through `linear()` without accumulators, every output bit."""
+    N, K = wl.QWEN3_8B_LINEARS[name]
+    x = wl.activations(M, K, seed=400 + M)
+    q, s = wl.weight_i8(N, K, seed=30 + SEEDS[name])
+    qt = pkg.QTensor(q.cuda(), s.cuda(), scheme="per_row_i8")
+    y = pkg.linear(x.cuda(), qt)
+    torch.cuda.synchronize()
+    yr, _, _, _ = oracle.linear_w8a8_f16(x.numpy(), q.numpy(), s.numpy(), None)
+    assert np.array_equal(_f16bits(y), yr.view(np.uint16))
+
+
+def test_prefill_bias_shipped_kernel(pkg, wl, cuda):
+    """Bias in the prefill epilogue, shipped instantiation, ragged M and N."""
+    M, N, K = 700, 1000, 1024
+    x = wl.activations(M, K, seed=41)
+    q, s = wl.weight_i8(N, K, seed=42)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(43)) * 3).half()
+    qt = pkg.QTensor(q.cuda(), s.cuda(), scheme="per_row_i8")
+    y = pkg.linear(x.cuda(), qt, bias.cuda())
+    torch.cuda.synchronize()
+    yr, _, _, _ = oracle.linear_w8a8_f16(x.numpy(), q.numpy(), s.numpy(), bias.numpy())
+    assert np.array_equal(_f16bits(y), yr.view(np.uint16))
+
+
 def test_quant_exhaustive_fp16(pkg, cuda):
     """Every fp16 bit pattern, in rows of 1024 (rows with inf/NaN get an inf/NaN
     scale), plus the same values under one fixed large scale."""

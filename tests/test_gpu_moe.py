@@ -83,6 +83,35 @@ def test_grouped_gemm_bitexact(pkg, wl, cuda, T, proj):
         assert np.array_equal(y.cpu().numpy()[rows].view(np.uint16), ys.view(np.uint16))
 
 
+@pytest.mark.parametrize("T", [256, 4096])
+@pytest.mark.parametrize("proj", ["gate_up", "down"])
+def test_grouped_gemm_shipped_kernel_rows(pkg, wl, cuda, T, proj):
+    """The grouped GEMM as SparseMoE runs it (no accumulator output), sampled
+    sorted rows against the oracle's per-expert GEMM, bit for bit."""
+    E, k, H, I = (wl.MOE[n] for n in ("experts", "top_k", "hidden", "inter"))
+    N, K = (2 * I, H) if proj == "gate_up" else (H, I)
+    _, topi = _routing(wl, T, E, k, seed=T + 5)
+    w, ws = wl.expert_weights(E, N, K, seed=13 if proj == "gate_up" else 14)
+    seg, rt, _ = pkg.moe_sort(topi.cuda(), E)
+    R = T * k
+    A = T if proj == "gate_up" else R
+    x = wl.activations(A, K, seed=T + 6)
+    aq, as_ = pkg.quantize_rowwise(x.cuda())
+    y = pkg.gemm_w8a8_grouped(aq, as_, w.cuda(), ws.cuda(), seg, R,
+                              row_index=rt if proj == "gate_up" else None)
+    torch.cuda.synchronize()
+    seg_r, rt_r, _, _ = oracle.moe_sort(topi.numpy(), E)
+    aq_r, as_r = oracle.quant_rowwise_f16(x.numpy())
+    rng = np.random.default_rng(T + 77)
+    rows = np.unique(np.concatenate([[0, R - 1], rng.choice(R, 64, replace=False)]))
+    expert = np.searchsorted(seg_r, rows, side="right") - 1
+    src = rt_r[rows] if proj == "gate_up" else rows
+    ys = np.stack([oracle.dequant_f16(oracle.gemm_i8(aq_r[s_:s_ + 1], w.numpy()[e]),
+                                      as_r[s_:s_ + 1], ws.numpy()[e])[0]
+                   for s_, e in zip(src, expert)])
+    assert np.array_equal(y.cpu().numpy()[rows].view(np.uint16), ys.view(np.uint16))
+
+
 _SPARSE = [0, 1, 0, 0, 33, 0, 2, 0, 0, 0, 0, 17, 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0, 0]
 
 
