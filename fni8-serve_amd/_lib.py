@@ -27,6 +27,7 @@ SIGNATURES = {
     "fni8_quantize_rowwise_f16": [_P, _I, _I, _I, _P, _I, _P, _P],
     "fni8_gemm_w8a8": [_P, _I, _P, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P],
     "fni8_linear_w8a8_f16": [_P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P],
+    "fni8_linear_w8a8_f16_noalloc": [_P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P],
     "fni8_moe_sort": [_P, _I, _I, _I, _P, _P, _P, _P],
     "fni8_gemm_w8a8_grouped": [_P, _P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _P, _P, _P],
     "fni8_moe_combine_f16": [_P, _I, _P, _P, _P, _I, _I, _P, _P],

@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace fni8h {
@@ -48,6 +50,44 @@ int check_device() {
                          prop.gcnArchName);
         return FNI8_ERR_DEVICE;
     }
+    return FNI8_OK;
+}
+
+// ---- scratch of fni8_linear_w8a8_f16_noalloc ---------------------------------
+// The quantized activations (int8 [M, K], row stride K) and their scales
+// (fp32 [M]) of the entry point that allocates nothing live in this array: one
+// copy per GPU, resident from the library's load on that GPU until the process
+// ends.  Every call on a GPU shares its copy (overlapping calls race).
+constexpr int64_t kNoAllocQBytes = (int64_t)48 << 20;  // M * K (every Qwen3-8B linear to M = 4096)
+constexpr int64_t kNoAllocRows = 65536;                // M
+static __device__ __align__(256) int8_t scratch[kNoAllocQBytes + kNoAllocRows * 4];
+
+// Device address of `scratch` on the current device, looked up once per device
+// with that device current (in host code `scratch` names a host-side stand-in,
+// not device memory).
+void* g_scratch_dev[kMaxDevices];
+std::mutex g_scratch_mu;
+
+int scratch_address(int8_t** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+        set_error_detail("no usable current device for the scratch lookup");
+        return FNI8_ERR_DEVICE;
+    }
+    void* p = __atomic_load_n(&g_scratch_dev[dev], __ATOMIC_ACQUIRE);
+    if (p == nullptr) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch_dev[dev];
+        if (p == nullptr) {
+            const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || p == nullptr) {
+                set_error_detail("scratch lookup on device %d: %s", dev, hipGetErrorString(e));
+                return FNI8_ERR_LAUNCH;
+            }
+            __atomic_store_n(&g_scratch_dev[dev], p, __ATOMIC_RELEASE);
+        }
+    }
+    *out = static_cast<int8_t*>(p);
     return FNI8_OK;
 }
 
@@ -103,6 +143,10 @@ int check_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr,
             FNI8_ERR_ALIGN, "fp16 operands misaligned");
     return FNI8_OK;
 }
+
+int linear_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                  const float* ws, int64_t N, const void* bias, void* y, int64_t ldy, int8_t* xq,
+                  float* xs, int32_t* acc_out, hipStream_t st);
 
 }  // namespace
 
@@ -179,7 +223,46 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
             FNI8_ERR_ALIGN, "scale/output pointers misaligned");
     rc = check_device();
     if (rc) return rc;
-    hipStream_t st = (hipStream_t)stream;
+    return linear_launch(x, ldx, M, K, w, ws, N, bias, y, ldy, xq, xs, acc_out,
+                         (hipStream_t)stream);
+}
+
+int fni8_linear_w8a8_f16_noalloc(const void* x, int64_t ldx, int64_t M, int64_t K,
+                                 const int8_t* w, const float* ws, int64_t N, const void* bias,
+                                 void* y, int64_t ldy, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(x && w && ws && y, FNI8_ERR_NULL, "x, w, ws and y are required");
+    int rc = check_gemm_shape(M, K, N);
+    if (rc) return rc;
+    REQUIRE(M <= kNoAllocRows && M * K <= kNoAllocQBytes, FNI8_ERR_SHAPE,
+            "M=%lld K=%lld exceeds the no-allocation scratch (M <= %lld and M*K <= %lld bytes)",
+            (long long)M, (long long)K, (long long)kNoAllocRows, (long long)kNoAllocQBytes);
+    REQUIRE(ldx >= K && ldy >= N, FNI8_ERR_STRIDE, "ldx=%lld < K or ldy=%lld < N",
+            (long long)ldx, (long long)ldy);
+    REQUIRE(aligned(x, 2) && aligned(w, 4) && aligned(ws, 4) && aligned(y, 2) && aligned(bias, 2),
+            FNI8_ERR_ALIGN, "x, w, ws, y or bias misaligned");
+    rc = check_device();
+    if (rc) return rc;
+    int8_t* sp = nullptr;
+    rc = scratch_address(&sp);
+    if (rc) return rc;
+    // xq: M rows of K bytes at the start; xs: M floats after the xq area.  Every
+    // byte the GEMM reads is written by this call's quantization first, so nothing
+    // needs clearing between calls.
+    return linear_launch(x, ldx, M, K, w, ws, N, bias, y, ldy, sp,
+                         reinterpret_cast<float*>(sp + kNoAllocQBytes), nullptr,
+                         (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The launches of the whole W8A8 linear on caller-checked arguments.
+int linear_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                  const float* ws, int64_t N, const void* bias, void* y, int64_t ldy, int8_t* xq,
+                  float* xs, int32_t* acc_out, hipStream_t st) {
+    int rc;
     // Decode sizes: one launch, the quantization fused into the GEMM -- on MFMA
     // for 3..4 tokens, as a dot4 GEMV for 1..2 (and shapes the MFMA kernel does
     // not take), where the streaming loop without an LDS pass is faster.
@@ -197,6 +280,10 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
     return fni8h::launch_gemm(xq, K, xs, nullptr, M, K, w, ws, N, 0, nullptr,
                               (const uint16_t*)bias, (uint16_t*)y, ldy, acc_out, st);
 }
+
+}  // namespace
+
+extern "C" {
 
 int fni8_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E, int32_t* seg_off,
                   int32_t* row_token, int32_t* pos, void* stream) {

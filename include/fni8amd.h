@@ -96,6 +96,23 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
                          int8_t* xq, float* xs, int32_t* acc_out, void* stream);
 
 /*
+ * fni8_linear_w8a8_f16 for callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation).  No
+ * counterpart in the reference.  Same arithmetic and output as
+ * fni8_linear_w8a8_f16 (without the accumulator output); the quantized
+ * activations and their scales go to a scratch array inside the library
+ * (48 MiB plus 256 KiB per GPU, resident until the process ends) instead of
+ * caller buffers, and the call allocates nothing.
+ *   Limits: M <= 65536 and M * K <= 48 MiB (every Qwen3-8B linear up to
+ *   M = 4096); larger shapes return FNI8_ERR_SHAPE.
+ *   Every call on a GPU shares that GPU's scratch: calls that overlap on one
+ *   GPU (different streams without ordering, several host threads) race.
+ */
+int fni8_linear_w8a8_f16_noalloc(const void* x, int64_t ldx, int64_t M, int64_t K,
+                                 const int8_t* w, const float* ws, int64_t N, const void* bias,
+                                 void* y, int64_t ldy, void* stream);
+
+/*
  * Routing sort for the grouped expert GEMM (replaces the per-expert
  * `mask = topi == e; mask.nonzero()` gathers of SparseMoE.forward,
  * fni8serve/models/moe.py:100-103).  A stable counting sort of the T*k

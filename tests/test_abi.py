@@ -54,6 +54,9 @@ def test_argument_errors_return_before_any_launch(lib):
     # NULL required pointer
     rc = lib.fni8_linear_w8a8_f16(None, 64, 1, 64, fake, fake, 8, None, fake, 8, fake, fake, None, None)
     assert rc == -1 and b"required" in lib.fni8_last_error()
+    # the entry point that allocates nothing: beyond its scratch (M * K > 48 MiB)
+    rc = lib.fni8_linear_w8a8_f16_noalloc(fake, 12288, 4097, 12288, fake, fake, 8, None, fake, 8, None)
+    assert rc == -2 and b"no-allocation scratch" in lib.fni8_last_error()
     # K not a multiple of 4 (the reference's quantizable rule, convert.py:128)
     rc = lib.fni8_linear_w8a8_f16(fake, 66, 1, 66, fake, fake, 8, None, fake, 8, fake, fake, None, None)
     assert rc == -2 and b"multiple of 4" in lib.fni8_last_error()
