@@ -46,6 +46,7 @@ sys.path.insert(0, ROOT)
 import __graft_entry__  # noqa: E402
 
 METRIC = "int8 TOPS & HBM GB/s (% of roofline), Qwen3-8B W8A8 linears M=1..4096, 1 GPU"
+ONE = {"shape": "gate_up", "m": 4096}   # --shape / --m of the prefill_one section
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 
@@ -204,15 +205,18 @@ def copy_calibration(device, mb=512):
     return {"bytes_each_way": mb << 20, "launches": 3}
 
 
-def load_traffic(root):
-    """Per-call HBM bytes of the decode linear measured by rocprofv3 counters,
-    kept as a text summary under profiles/ (null when absent)."""
-    path = os.path.join(root, "profiles", "decode_linear_hbm_traffic.json")
+def load_json(path):
+    """A summary kept under profiles/ (null when absent)."""
     try:
         with open(path) as f:
             return json.load(f)
     except (OSError, ValueError):
         return None
+
+
+def load_traffic(root):
+    """Per-call HBM bytes of the decode linear measured by rocprofv3 counters."""
+    return load_json(os.path.join(root, "profiles", "decode_linear_hbm_traffic.json"))
 
 
 def time_eager(fn, reps):
@@ -228,25 +232,82 @@ def time_eager(fn, reps):
 
 
 def prefill_section(pkg, wl, pool, device, ms=(512, 2048, 4096)):
+    """Prefill linears on the four shapes at M in {512, 2048, 4096}: the whole
+    `linear()` call, and its two launches alone -- the per-token quantization
+    and the int8 GEMM (with its fused epilogue) on already-quantized rows.
+    Weights rotate over 8 layers of distinct copies.  Flat keys (one scalar
+    each): <shape>_M<M>_{us, gemm_us, quant_us, TOPS, gemm_TOPS, pct_mfma_peak}."""
     out = {}
     layers = pool[:8]
     for M in ms:
         xs = {K: wl.activations(M, K, seed=300 + M, device="cpu").to(device) for K in (4096, 12288)}
+        qs = {K: pkg.quantize_rowwise(x) for K, x in xs.items()}
         for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
             idx = [0]
 
-            def fn(name=name, K=K):
+            def whole(name=name, K=K):
                 qt = layers[idx[0] % len(layers)][name]
                 idx[0] += 1
                 pkg.linear(xs[K], qt)
-            t = min(time_burst(fn, reps=8) for _ in range(3))
+
+            def gemm(name=name, K=K):
+                qt = layers[idx[0] % len(layers)][name]
+                idx[0] += 1
+                pkg.gemm_w8a8(qs[K][0], qs[K][1], qt)
+
+            def quant(K=K):
+                pkg.quantize_rowwise(xs[K])
+            t = min(time_burst(whole, reps=8) for _ in range(3))
+            tg = min(time_burst(gemm, reps=8) for _ in range(3))
+            tq = min(time_burst(quant, reps=8) for _ in range(3))
             ops = wl.linear_ops(M, N, K)
-            b = wl.linear_bytes(M, N, K)
-            out[f"{name}_M{M}"] = {"us": round(t * 1e6, 2), "TOPS": round(ops / t / 1e12, 1),
-                                   "pct_mfma_peak": round(ops / t / 1e12 / INT8_PEAK_TOPS * 100, 1),
-                                   "GBps": round(b / t / 1e9, 1)}
-        del xs
+            key = f"{name}_M{M}"
+            out[f"{key}_us"] = round(t * 1e6, 2)
+            out[f"{key}_gemm_us"] = round(tg * 1e6, 2)
+            out[f"{key}_quant_us"] = round(tq * 1e6, 2)
+            out[f"{key}_TOPS"] = round(ops / t / 1e12, 1)
+            out[f"{key}_gemm_TOPS"] = round(ops / tg / 1e12, 1)
+            out[f"{key}_pct_mfma_peak"] = round(ops / t / 1e12 / INT8_PEAK_TOPS * 100, 1)
+        del xs, qs
     return out
+
+
+def prefill_roofline(wl, prefill, M=4096):
+    """The MFMA-bound roofline entry: the prefill GEMM kernel at M = 4096 over the
+    four Qwen3-8B shapes (one launch each; the quantize launch is reported beside
+    it).  achieved = sum of 2*M*N*K / sum of the GEMM launch times."""
+    ops = t = tq = 0.0
+    for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
+        ops += wl.linear_ops(M, N, K)
+        t += prefill[f"{name}_M{M}_gemm_us"] * 1e-6
+        tq += prefill[f"{name}_M{M}_quant_us"] * 1e-6
+    achieved = ops / t / 1e12
+    r = {"kernel": "gemm_pp_kernel (prefill int8 GEMM + fused dequant epilogue), Qwen3-8B "
+                   f"QKV/O/gate_up/down at M = {M}",
+         "bound": "mfma", "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS",
+         "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
+         "avg_launch_us": round(t / 4 * 1e6, 2), "algorithmic_ops_per_launch": int(ops / 4),
+         "quant_avg_launch_us": round(tq / 4 * 1e6, 2),
+         "with_quant_TOPS": round(ops / (t + tq) / 1e12, 1)}
+    for name in wl.QWEN3_8B_LINEARS:
+        r[f"frac_{name}"] = round(prefill[f"{name}_M{M}_gemm_TOPS"] / INT8_PEAK_TOPS, 4)
+    tr = load_json(os.path.join(ROOT, "profiles", "prefill_gemm_hbm_traffic.json"))
+    if tr is not None and "hbm_bytes_per_launch" in tr:
+        r["traffic"] = tr["hbm_bytes_per_launch"]
+    return r
+
+
+def prefill_one(pkg, wl, pool, device, name, M, reps=8):
+    """One prefill shape only (for per-shape profiler runs): `reps` linear() calls
+    over the pool's layers, after one warm call."""
+    N, K = wl.QWEN3_8B_LINEARS[name]
+    x = wl.activations(M, K, seed=300 + M, device="cpu").to(device)
+    pkg.linear(x, pool[0][name])
+    torch.cuda.synchronize()
+    for i in range(reps):
+        pkg.linear(x, pool[(i + 1) % len(pool)][name])
+    torch.cuda.synchronize()
+    return {"shape": name, "M": M, "N": N, "K": K, "calls": reps + 1}
 
 
 def moe_section(pkg, wl, device, ts=(16, 256, 4096)):
@@ -546,47 +607,145 @@ def load_section(pkg, pool, device, layers=2, reps=3):
         shutil.rmtree(d, ignore_errors=True)
 
 
+def _err_stats(y: torch.Tensor, exact: torch.Tensor):
+    """max |y - exact| and max |y - exact| / |exact| over outputs whose exact value
+    is a normal fp16 number (relative error is meaningless around 0)."""
+    y = y.double()
+    fin = torch.isfinite(exact) & (exact.abs() < 65504.0)
+    err = (y - exact).abs()[fin]
+    norm = fin & (exact.abs() >= 2.0 ** -14)
+    rel = ((y - exact).abs()[norm] / exact.abs()[norm])
+    return (float(err.max()) if err.numel() else 0.0, float(rel.max()) if rel.numel() else 0.0)
+
+
+def fp16_error_section(pkg, wl, device):
+    """Error of the fp16 outputs against the fp64 closed form of the epilogue:
+    exact = acc * xs[m] * ws[n], with acc the exact int32 product of the
+    kernel's own int8 activations (torch._int_mm on the CPU), i.e. what the
+    epilogue's roundings cost (the bound is one fp16 rounding, relative 2^-11,
+    plus fp32 roundings of the scale products).  cfg1 and cfg2 cover every
+    output; cfg3 32 sampled rows per shape; cfg4 64 sampled sorted rows of the
+    grouped gate_up projection.  Flat keys <config>_max_abs / <config>_max_rel."""
+    out = {}
+    cases = [("cfg1_qwen3_0p6b_gate_up_M8", 8, wl.CPU_CASE["N"], wl.CPU_CASE["K"], False)]
+    for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
+        cases.append((f"cfg2_{name}_M16", 16, N, K, False))
+        cases.append((f"cfg3_{name}_M4096", 4096, N, K, True))
+    for i, (tag, M, N, K, sample) in enumerate(cases):
+        x = wl.activations(M, K, seed=1000 + i, device="cpu")
+        q, s = wl.weight_i8(N, K, seed=1100 + i)
+        qt = pkg.QTensor(q.to(device), s.to(device), scheme="per_row_i8")
+        y, xq, xsc, _ = pkg.linear_with_intermediates(x.to(device), qt)
+        rows = torch.arange(M)
+        if sample:
+            rows = torch.unique(torch.cat([torch.tensor([0, M - 1]),
+                                           torch.randperm(M, generator=torch.Generator().manual_seed(i))[:30]]))
+        acc = torch._int_mm(xq.cpu()[rows], q.t())
+        exact = acc.double() * xsc.cpu()[rows].double()[:, None] * s.double()[None, :]
+        out[f"{tag}_max_abs"], out[f"{tag}_max_rel"] = _err_stats(y.cpu()[rows], exact)
+    E, k, H, I = (wl.MOE[n] for n in ("experts", "top_k", "hidden", "inter"))
+    T = 256
+    topw, topi = wl.route(wl.router_logits(T, E, seed=T + 1), k)
+    w, ws = wl.expert_weights(E, 2 * I, H, seed=1200)
+    x = wl.activations(T, H, seed=1201, device="cpu")
+    seg, rt, _ = pkg.moe_sort(topi.to(device), E)
+    xq, xsc = pkg.quantize_rowwise(x.to(device))
+    y = pkg.gemm_w8a8_grouped(xq, xsc, w.to(device), ws.to(device), seg, T * k, row_index=rt)
+    seg, rt, xq, xsc, y = seg.cpu(), rt.cpu(), xq.cpu(), xsc.cpu(), y.cpu()
+    rows = torch.randperm(T * k, generator=torch.Generator().manual_seed(7))[:64]
+    expert = torch.searchsorted(seg, rows, right=True) - 1
+    ys, ex = [], []
+    for r, e in zip(rows.tolist(), expert.tolist()):
+        src = int(rt[r])
+        acc = torch._int_mm(xq[src:src + 1], w[e].t())
+        ex.append(acc.double()[0] * float(xsc[src]) * ws[e].double())
+        ys.append(y[r])
+    out["cfg4_gate_up_T256_max_abs"], out["cfg4_gate_up_T256_max_rel"] = _err_stats(
+        torch.stack(ys), torch.stack(ex))
+    return {key: float(f"{v:.4g}") for key, v in out.items()}
+
+
+def _time_cpu(fn, min_s, min_calls=3):
+    fn()  # warm
+    calls, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        el = time.perf_counter() - t0
+        if calls >= min_calls and el >= min_s:
+            return el / calls
+
+
 def cpu_baseline(wl, budget_s=40.0, per_linear_s=0.8):
-    """The reference's CPU linear (dequantize W per call, then F.linear in fp16),
-    on one layer's four linears at M in {1, 4, 16, 64}: each linear is called
-    repeatedly for about `per_linear_s` seconds after a warm call (about 13 s of
-    CPU work in all), and the mean time per call is used."""
+    """CPU baselines on all host cores, timed on this machine in the same run.
+
+    Path 1, the headline `value`: the reference's own CPU linear -- dequantize W
+    to fp16 on every call, then F.linear in fp16 (fni8serve/layers/linear.py:28-31,
+    :70-71) -- on one layer's four Qwen3-8B linears at M in {1, 4, 16, 64}; each
+    called repeatedly for about `per_linear_s` seconds after a warm call, mean per
+    call (about 13 s of CPU work in all).  Path 2: the W8A8 arithmetic on the CPU
+    -- the oracle's per-token quantization and fp32 epilogue (plain C) around an
+    exact int32 GEMM (torch._int_mm) -- on the same sample.  Both paths also on
+    the Qwen3-0.6B gate_up linear at M = 8 (cfg1) and on one prefill linear
+    (O, M = 512).  Flat scalar keys."""
+    from oracle import oracle
     from oracle.reference_cpu import reference_cpu_linear
 
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    tot_b, tot_t, done = 0, 0.0, []
+
+    def path2(x, q, s, qT):
+        xq, xs = oracle.quant_rowwise_f16(x.numpy())
+        acc = torch._int_mm(torch.from_numpy(xq), qT)
+        return oracle.dequant_f16(acc.numpy(), xs, s.numpy())
+
+    tot_b, tot_t1, tot_t2, done = 0, 0.0, 0.0, []
     t_start = time.perf_counter()
     for M in (1, 4, 16, 64):
         for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
             if time.perf_counter() - t_start > budget_s:
                 break
             q, s = wl.weight_i8(N, K, seed=11)
+            qT = q.t()   # [K, N] view: the weight as stored, no copy
             x = wl.activations(M, K, seed=12)
-            reference_cpu_linear(x, q, s)  # warm
-            calls, t0 = 0, time.perf_counter()
-            while True:
-                reference_cpu_linear(x, q, s)
-                calls += 1
-                el = time.perf_counter() - t0
-                if calls >= 3 and el >= per_linear_s:
-                    break
-            dt = el / calls
+            tot_t1 += _time_cpu(lambda: reference_cpu_linear(x, q, s), per_linear_s)
+            tot_t2 += _time_cpu(lambda: path2(x, q, s, qT), per_linear_s / 2)
             tot_b += wl.linear_bytes(M, N, K)
-            tot_t += dt
             done.append(f"{name}@M{M}")
+    res = {}
+    c = wl.CPU_CASE
+    q, s = wl.weight_i8(c["N"], c["K"], seed=8)
+    x = wl.activations(c["M"], c["K"], seed=7)
+    t1 = _time_cpu(lambda: reference_cpu_linear(x, q, s), 0.5)
+    t2 = _time_cpu(lambda: path2(x, q, s, q.t()), 0.5)
+    ops, b = wl.linear_ops(c["M"], c["N"], c["K"]), wl.linear_bytes(c["M"], c["N"], c["K"])
+    res.update({"cfg1_path1_us": round(t1 * 1e6, 1), "cfg1_path2_us": round(t2 * 1e6, 1),
+                "cfg1_path1_GBps": round(b / t1 / 1e9, 3), "cfg1_path2_GBps": round(b / t2 / 1e9, 3)})
+    N, K = wl.QWEN3_8B_LINEARS["o"]
+    q, s = wl.weight_i8(N, K, seed=13)
+    x = wl.activations(512, K, seed=14)
+    t1 = _time_cpu(lambda: reference_cpu_linear(x, q, s), 1.0, min_calls=2)
+    t2 = _time_cpu(lambda: path2(x, q, s, q.t()), 1.0, min_calls=2)
+    ops = wl.linear_ops(512, N, K)
+    res.update({"prefill_o_M512_path1_TOPS": round(ops / t1 / 1e12, 3),
+                "prefill_o_M512_path2_TOPS": round(ops / t2 / 1e12, 3)})
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
             model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
         pass
-    return {"value": round(tot_b / tot_t / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"reference CPU path (fp16 dequant of W per call + F.linear), one layer: "
-                      f"{len(done)} linears ({', '.join(done)}), each called repeatedly for "
-                      f"~{per_linear_s} s after a warm call (mean per call), {tot_t:.3f} s of "
-                      f"per-call time summed, cpu '{model}', os.cpu_count={os.cpu_count()}"}
+    out = {"value": round(tot_b / tot_t1 / 1e9, 3), "unit": "GB/s", "cores": threads,
+           "kind": "port",
+           "sample": f"reference CPU path (fp16 dequant of W per call + F.linear), one layer: "
+                     f"{len(done)} linears ({', '.join(done)}), each called repeatedly for "
+                     f"~{per_linear_s} s after a warm call (mean per call), {tot_t1:.3f} s of "
+                     f"per-call time summed, cpu '{model}', os.cpu_count={os.cpu_count()}",
+           "path2_GBps": round(tot_b / tot_t2 / 1e9, 3),
+           "path2": "W8A8 on the CPU: oracle quantization and epilogue (C) + torch._int_mm, "
+                    "same sample"}
+    out.update(res)
+    return out
 
 
 def main():
@@ -595,7 +754,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--layers", type=int, default=36)
-    ap.add_argument("--sections", default="roofline,prefill,w4a8,moe,moe_layer,stack,fusion,load,cpu")
+    ap.add_argument("--sections",
+                    default="roofline,prefill,w4a8,moe,moe_layer,stack,fusion,load,fp16_error,cpu")
+    ap.add_argument("--shape", default="gate_up", help="prefill_one: linear name")
+    ap.add_argument("--m", type=int, default=4096, help="prefill_one: rows")
     ap.add_argument("--no-step", action="store_true",
                     help="skip the graph-replayed decode step (for counter runs of one section)")
     args = ap.parse_args()
@@ -604,6 +766,7 @@ def main():
               "is single-GPU; multi-GPU sharding is a design note only)", file=sys.stderr)
         sys.exit(2)
     sections = set(s for s in args.sections.split(",") if s)
+    ONE["shape"], ONE["m"] = args.shape, args.m
 
     pkg = __graft_entry__.load_package()
     from importlib import import_module
@@ -676,7 +839,14 @@ def run_sections(result, sections, pkg, wl, pool, device):
         result["copy_calibration"] = copy_calibration(device)
     if "prefill" in sections:
         result["prefill"] = prefill_section(pkg, wl, pool, device)
+        result["roofline_prefill"] = prefill_roofline(wl, result["prefill"])
         log(f"prefill: {result['prefill']}")
+        log(f"roofline_prefill: {result['roofline_prefill']}")
+    if "prefill_one" in sections:
+        result["prefill_one"] = prefill_one(pkg, wl, pool, device, ONE["shape"], ONE["m"])
+    if "fp16_error" in sections:
+        result["fp16_error"] = fp16_error_section(pkg, wl, device)
+        log(f"fp16_error: {result['fp16_error']}")
     if "moe" in sections:
         result["moe"] = moe_section(pkg, wl, device)
         log(f"moe: {result['moe']}")

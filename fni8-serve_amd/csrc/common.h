@@ -261,12 +261,11 @@ int launch_tile32(const int8_t* aq, int64_t lda, const float* as, const int32_t*
                   int64_t M, int64_t K, const int8_t* w, const float* ws, int64_t N, int64_t E,
                   const int32_t* seg_off, const uint16_t* bias, uint16_t* y, int64_t ldy,
                   int32_t* acc_out, hipStream_t st);
-// Prefill GEMM, two wave groups taking turns at MFMA and memory work (K % 128 == 0);
-// returns 1 when not taken.
-int launch_pp(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index, int64_t M,
-              int64_t K, const int8_t* w, const float* ws, int64_t N, int64_t E,
-              const int32_t* seg_off, const uint16_t* bias, uint16_t* y, int64_t ldy,
-              int32_t* acc_out, hipStream_t st);
+// Dense prefill GEMM, two wave groups taking turns at MFMA and memory work
+// (K % 128 == 0); returns 1 when not taken.
+int launch_pp(const int8_t* aq, int64_t lda, const float* as, int64_t M, int64_t K,
+              const int8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
+              int64_t ldy, int32_t* acc_out, hipStream_t st);
 int launch_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E, int32_t* seg_off,
                     int32_t* row_token, int32_t* pos, hipStream_t st);
 int launch_moe_combine(const uint16_t* yr, int64_t H, const int32_t* topi,

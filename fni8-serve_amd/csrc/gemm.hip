@@ -476,13 +476,8 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
                 else launch_skinny<1, 1, 2, 8, true>(a, slots, st);
             }
         } else {
-            rc = 1;
-            if (avg >= 128.0)
-                rc = launch_pp(aq, lda, as, row_index, M, K, w, ws, N, E, seg_off, bias, y, ldy,
+            rc = launch_tile32(aq, lda, as, row_index, M, K, w, ws, N, E, seg_off, bias, y, ldy,
                                acc_out, st);
-            if (rc == 1)
-                rc = launch_tile32(aq, lda, as, row_index, M, K, w, ws, N, E, seg_off, bias, y,
-                                   ldy, acc_out, st);
             if (rc == 1) {
                 const unsigned slots = (unsigned)((M + 127) / 128 + E);
                 rc = launch_tile<128, 128, 2, 2, true>(a, slots, st);
@@ -496,8 +491,7 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
             launch_decode(a, st);
         }
     } else {
-        rc = launch_pp(aq, lda, as, row_index, M, K, w, ws, N, 0, seg_off, bias, y, ldy, acc_out,
-                       st);
+        rc = launch_pp(aq, lda, as, M, K, w, ws, N, bias, y, ldy, acc_out, st);
         if (rc == 1)
             rc = launch_tile32(aq, lda, as, row_index, M, K, w, ws, N, 0, seg_off, bias, y, ldy,
                                acc_out, st);

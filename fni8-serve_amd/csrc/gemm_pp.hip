@@ -44,12 +44,6 @@ __device__ __forceinline__ void copy16_s(uint32_t lds, const int8_t* base, uint3
                  :: "s"(lds), "v"(voff), "s"(base) : "memory", "m0");
 }
 
-// the same from a per-lane 64-bit address
-__device__ __forceinline__ void copy16_v(uint32_t lds, const int8_t* p) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-                 :: "s"(lds), "v"(p) : "memory", "m0");
-}
-
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
@@ -62,11 +56,10 @@ __device__ __forceinline__ void slot_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int BM, int BN, bool GROUPED, bool WRITE_ACC>
+template <int BM, int BN, bool WRITE_ACC>
 __global__ __launch_bounds__(512) void gemm_pp_kernel(
-    const int8_t* __restrict__ aq, int64_t lda, const float* __restrict__ as,
-    const int32_t* __restrict__ row_index, int M, int K, const int8_t* __restrict__ w,
-    const float* __restrict__ ws, int N, int E, const int32_t* __restrict__ seg_off,
+    const int8_t* __restrict__ aq, int64_t lda, const float* __restrict__ as, int M, int K,
+    const int8_t* __restrict__ w, const float* __restrict__ ws, int N,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy,
     int32_t* __restrict__ acc_out) {
     constexpr int BK = 128, CPR = BK / 16;   // bytes and 16-byte chunks per row per k-tile
@@ -82,31 +75,13 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     const int g = wave >> 2, s = wave & 3;
 
     int m0, m1, n0;
-    const int8_t* wexp = w;
-    const float* wsexp = ws;
-    const uint16_t* bexp = bias;
-    if constexpr (GROUPED) {  // x = segment tile slot, y = n-tile
-        n0 = blockIdx.y * BN;
-        int e;
-        const bool found = fni8::find_group_tile(seg_off, E, BM, blockIdx.x, M, e, m0, m1);
-        // the lookup is wave-uniform; say so, so the copy bases stay in SGPRs
-        if (!__builtin_amdgcn_readfirstlane((int)found)) return;
-        e = __builtin_amdgcn_readfirstlane(e);
-        m0 = __builtin_amdgcn_readfirstlane(m0);
-        m1 = __builtin_amdgcn_readfirstlane(m1);
-        wexp += (int64_t)e * N * K;
-        wsexp += (int64_t)e * N;
-        if (bias) bexp += (int64_t)e * N;
-    } else {
-        fni8t::dense_tile<BM, BN>(M, N, m0, m1, n0);
-    }
+    fni8t::dense_tile<BM, BN>(M, N, m0, m1, n0);
     const int KT = K / BK;
 
     // Copy sources.  Instruction i of wave w fills stage slots [(w*D+i)*64, +64)
     // (16-byte slots; row = slot / 8); rows past the tile's end repeat its last
     // row (their products land in rows that are never stored).
     uint32_t voff[D];
-    const int8_t* aptr[GROUPED ? D : 1];
 #pragma unroll
     for (int i = 0; i < D; i++) {
         const int slot = (wave * D + i) * 64 + lane;
@@ -115,37 +90,25 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
             const int c = p ^ ((row >> 1) & 7);
             int mr = m0 + row;
             mr = mr < m1 ? mr : m1 - 1;
-            if constexpr (GROUPED) {
-                const int src = row_index != nullptr ? row_index[mr] : mr;
-                aptr[i] = aq + (int64_t)src * lda + c * 16;
-                voff[i] = 0;
-            } else {
-                voff[i] = (uint32_t)((int64_t)(mr - m0) * lda + c * 16);
-            }
+            voff[i] = (uint32_t)((int64_t)(mr - m0) * lda + c * 16);
         } else {
             const int rb = row - BM;
             const int c = p ^ ((rb >> 1) & 7);
             int nr = n0 + rb;
             nr = nr < N ? nr : N - 1;
             voff[i] = (uint32_t)((int64_t)(nr - n0) * K + c * 16);
-            if constexpr (GROUPED) aptr[i] = nullptr;
         }
     }
     const int8_t* abase = aq + (int64_t)m0 * lda;
-    const int8_t* bbase = wexp + (int64_t)n0 * K;
+    const int8_t* bbase = w + (int64_t)n0 * K;
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
     auto issue = [&](int t, int stage) {
 #pragma unroll
         for (int i = 0; i < D; i++) {
             const uint32_t l = lds0 + stage * STAGE + (wave * D + i) * 1024;
-            const bool a_ins = wave * D + i < AINS;   // wave-uniform
-            if constexpr (GROUPED) {
-                if (a_ins) copy16_v(l, aptr[i] + t * BK);
-                else copy16_s(l, bbase + t * BK, voff[i]);
-            } else {
-                // one instruction, its base chosen by a scalar select (no branch)
-                copy16_s(l, (a_ins ? abase : bbase) + t * BK, voff[i]);
-            }
+            // one instruction, its base chosen by a scalar select (wave-uniform)
+            const bool a_ins = wave * D + i < AINS;
+            copy16_s(l, (a_ins ? abase : bbase) + t * BK, voff[i]);
         }
     };
 
@@ -229,26 +192,24 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     if (g == 0) slot_barrier();
     __syncthreads();  // every copy has landed and every wave is done with the stages
 
-    fni8t::tile_epilogue<BM, BN, GROUPED, WRITE_ACC>(acc, smem, tid, lane, g, s, m0, m1, n0, N,
-                                                     row_index, as, wsexp, bexp, y, ldy, acc_out);
+    fni8t::tile_epilogue<BM, BN, false, WRITE_ACC>(acc, smem, tid, lane, g, s, m0, m1, n0, N,
+                                                   nullptr, as, ws, bias, y, ldy, acc_out);
 }
 
-template <int BM, int BN, bool GROUPED>
-int launch(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index, int M,
-           int K, const int8_t* w, const float* ws, int N, int E, const int32_t* seg_off,
-           const uint16_t* bias, uint16_t* y, int64_t ldy, int32_t* acc_out, unsigned slots,
-           hipStream_t st) {
+template <int BM, int BN>
+int launch(const int8_t* aq, int64_t lda, const float* as, int M, int K, const int8_t* w,
+           const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
+           int32_t* acc_out, hipStream_t st) {
     constexpr size_t main_lds = (size_t)2 * (BM + BN) * 128;
     constexpr size_t epi_lds = fni8t::tile_epilogue_lds<BM, BN>();
     constexpr size_t lds = main_lds > epi_lds ? main_lds : epi_lds;
     static_assert(lds <= 160 * 1024, "LDS budget");
-    const unsigned ntn = (unsigned)((N + BN - 1) / BN);
-    const dim3 grid = GROUPED ? dim3(slots, ntn) : dim3(ntn * (unsigned)((M + BM - 1) / BM));
+    const dim3 grid(((N + BN - 1) / BN) * (unsigned)((M + BM - 1) / BM));
     // The LDS limit is a per-function attribute: each instantiation sets it once
     // (a repeated set with the same value is harmless).
     auto run = [&](auto acc_c) -> int {
         constexpr bool ACC = decltype(acc_c)::value;
-        const auto kern = gemm_pp_kernel<BM, BN, GROUPED, ACC>;
+        const auto kern = gemm_pp_kernel<BM, BN, ACC>;
         static bool attr_set = false;
         if (!attr_set) {
             hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -259,8 +220,8 @@ int launch(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_in
             }
             attr_set = true;
         }
-        hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, aq, lda, as, row_index, M, K, w, ws, N,
-                           E, seg_off, bias, y, ldy, acc_out);
+        hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, aq, lda, as, M, K, w, ws, N, bias, y,
+                           ldy, acc_out);
         return FNI8_OK;
     };
     if (acc_out) return run(std::true_type{});
@@ -284,24 +245,21 @@ int cu_count() {
 namespace fni8h {
 
 // Returns 1 when the shape is not taken (the caller falls back), else an FNI8 code.
-// Needs K % 128 == 0 and 16-byte aligned operand rows.  Dense tiles: the shape
-// from {256x256, 128x256, 256x128} with the least estimated time, counting
+// Dense only; needs K % 128 == 0 and 16-byte aligned operand rows.  Tiles: the
+// shape from {256x256, 128x256, 256x128} with the least estimated time, counting
 // whole rounds of one workgroup per CU and the lower MFMA rate of the smaller
 // tiles (each of their k-tiles moves 3/4 of the bytes for 1/2 of the products).
-int launch_pp(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index, int64_t M,
-              int64_t K, const int8_t* w, const float* ws, int64_t N, int64_t E,
-              const int32_t* seg_off, const uint16_t* bias, uint16_t* y, int64_t ldy,
-              int32_t* acc_out, hipStream_t st) {
+// Expert segments stay on the 32x32x32 tile kernel: the MoE projections have
+// short K (768 and 2048 bytes, 6 and 16 k-tiles), where a grouped form of this
+// kernel (128x256 segment tiles) measured 18% slower at T = 4096 (473 against
+// 399 us for gate_up + down) -- its pipeline and epilogue are not amortised.
+int launch_pp(const int8_t* aq, int64_t lda, const float* as, int64_t M, int64_t K,
+              const int8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
+              int64_t ldy, int32_t* acc_out, hipStream_t st) {
     if (K % 128 != 0 || lda % 16 != 0 || ((uintptr_t)aq & 15) || ((uintptr_t)w & 15)) return 1;
-    // per-lane copy offsets are 32-bit: a tile's B rows (and dense A rows) span
-    // at most 256 rows
+    // per-lane copy offsets are 32-bit: a tile's rows span at most 256 rows
     if (256 * K >= ((int64_t)1 << 32) || 256 * lda >= ((int64_t)1 << 32)) return 1;
-    const int m = (int)M, k = (int)K, n = (int)N, e = (int)E;
-    if (E > 0) {
-        const unsigned slots = (unsigned)((M + 255) / 256 + E);
-        return launch<256, 256, true>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off, bias, y,
-                                      ldy, acc_out, slots, st);
-    }
+    const int m = (int)M, k = (int)K, n = (int)N;
     const int cus = cu_count();
     constexpr int kTiles[3][2] = {{256, 256}, {128, 256}, {256, 128}};
     constexpr double kCost[3] = {1.0, 0.5 / 0.75, 0.5 / 0.75};   // relative time of one tile
@@ -315,16 +273,15 @@ int launch_pp(const int8_t* aq, int64_t lda, const float* as, const int32_t* row
             best = i;
         }
     }
+    // Too few workgroups for these tiles (prefill M = 512): the caller's
+    // smaller-tile kernel fills the CUs better.
+    const int64_t wgs = ((M + kTiles[best][0] - 1) / kTiles[best][0]) *
+                        ((N + kTiles[best][1] - 1) / kTiles[best][1]);
+    if (4 * wgs < 3 * (int64_t)cus) return 1;
     switch (best) {
-        case 0:
-            return launch<256, 256, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
-                                           bias, y, ldy, acc_out, 0, st);
-        case 1:
-            return launch<128, 256, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
-                                           bias, y, ldy, acc_out, 0, st);
-        default:
-            return launch<256, 128, false>(aq, lda, as, row_index, m, k, w, ws, n, e, seg_off,
-                                           bias, y, ldy, acc_out, 0, st);
+        case 0: return launch<256, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
+        case 1: return launch<128, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
+        default: return launch<256, 128>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
     }
 }
 
