@@ -24,6 +24,14 @@ captured in a HIP graph:
 Because quantization is row-local and the GEMM is exact, every int8 row, int32
 accumulator and fp16 expert output equals what the per-expert loop computes.
 CPU inputs run the reference's loop unchanged.
+
+Experts of another scheme (per_group_i4 int4 weights, as the reference's
+converter writes for weight_bits=4, fni8serve/convert.py:130-131) keep their
+own GatedMLP modules (moe.py:56).  On the GPU they run on the same device
+routing and sort, then each non-empty expert's sorted rows go through its
+GatedMLP (the W4A8 kernels) and the same combine: one host read of the segment
+offsets per layer instead of the reference's two syncs per expert, and the
+same per-expert arithmetic and index_add_ order.
 """
 from __future__ import annotations
 
@@ -58,13 +66,20 @@ class SparseMoE(nn.Module):
             e_score_correction_bias.float() if e_score_correction_bias is not None else None,
             persistent=False)
         self.num_experts = len(experts)
-        # Stacked expert weights [E, N, K] / scales [E, N] for the grouped kernel;
-        # the per-expert modules keep views into the same storage.
         gu = [e[0] for e in experts]
         dn = [e[1] for e in experts]
-        for q in gu + dn:
-            if q.scheme != "per_row_i8":
-                raise ValueError(f"grouped expert GEMM needs per_row_i8 weights, got {q.scheme!r}")
+        self.act_fn = get_act_and_mul(act)
+        self.shared = GatedMLP(*shared_expert, act=act) if shared_expert else None
+        self.shared_gate = (nn.Parameter(shared_expert_gate)
+                            if shared_expert_gate is not None else None)
+        self.grouped = all(q.scheme == "per_row_i8" for q in gu + dn)
+        if not self.grouped:
+            # per_group_i4 (or mixed) experts: one GatedMLP per expert on its own
+            # QTensors, as the reference builds them (moe.py:56)
+            self.experts = nn.ModuleList([GatedMLP(g_, d_, act=act) for g_, d_ in experts])
+            return
+        # Stacked expert weights [E, N, K] / scales [E, N] for the grouped kernel;
+        # the per-expert modules keep views into the same storage.
         self.register_buffer("w_gate_up", torch.stack([q.data for q in gu]).contiguous(),
                              persistent=False)
         self.register_buffer("s_gate_up",
@@ -79,10 +94,6 @@ class SparseMoE(nn.Module):
             GatedMLP(QTensor(self.w_gate_up[e], self.s_gate_up[e], scheme="per_row_i8"),
                      QTensor(self.w_down[e], self.s_down[e], scheme="per_row_i8"), act=act)
             for e in range(self.num_experts)])
-        self.act_fn = get_act_and_mul(act)
-        self.shared = GatedMLP(*shared_expert, act=act) if shared_expert else None
-        self.shared_gate = (nn.Parameter(shared_expert_gate)
-                            if shared_expert_gate is not None else None)
 
     def _gate_f32(self) -> torch.Tensor:
         """The router weight in fp32 (moe.py:64 converts it on every call); the
@@ -145,6 +156,21 @@ class SparseMoE(nn.Module):
         y = ops.gemm_w8a8_grouped(aq, as_, self.w_down, self.s_down, seg_off, R)
         return ops.moe_combine(y, topi, topw, pos)
 
+    def experts_sorted(self, xf: torch.Tensor, topw: torch.Tensor, topi: torch.Tensor):
+        """Experts that are not per_row_i8 (the W4A8 path): device sort, one host
+        read of the segment offsets, each non-empty expert's GatedMLP on its
+        sorted rows (ascending token, then slot: the rows nonzero() gives it at
+        moe.py:103), then the device combine in ascending expert order."""
+        R = xf.shape[0] * self.top_k
+        seg_off, row_token, pos = ops.moe_sort(topi, self.num_experts)
+        y = torch.empty((R, xf.shape[1]), dtype=xf.dtype, device=xf.device)
+        bounds = seg_off.tolist()
+        for e in range(self.num_experts):
+            lo, hi = bounds[e], bounds[e + 1]
+            if hi > lo:
+                y[lo:hi] = self.experts[e](xf[row_token[lo:hi].long()])
+        return ops.moe_combine(y, topi, topw, pos)
+
     def _experts_loop(self, xf: torch.Tensor, topw: torch.Tensor, topi: torch.Tensor):
         """The reference's per-expert loop (moe.py:97-105), for CPU inputs."""
         out = torch.zeros_like(xf)
@@ -162,7 +188,8 @@ class SparseMoE(nn.Module):
         xf = x.reshape(-1, H)
         topw, topi = self.route(xf)
         if xf.is_cuda:
-            out = self.experts_grouped(xf, topw, topi)
+            out = (self.experts_grouped(xf, topw, topi) if self.grouped
+                   else self.experts_sorted(xf, topw, topi))
         else:
             out = self._experts_loop(xf, topw, topi)
         if self.shared is not None:

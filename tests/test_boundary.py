@@ -177,6 +177,32 @@ def test_sparse_moe_cpu_loop_and_routing(pkg):
     assert moe.w_gate_up.shape == (4, 64, 64) and moe.w_down.shape == (4, 64, 32)
 
 
+def test_sparse_moe_w4_experts_cpu_loop(pkg):
+    """per_group_i4 experts build (no stacking) and run the reference's CPU loop
+    through each expert's GatedMLP (dequantized int4 weights, linear.py:32-45)."""
+    g = torch.Generator().manual_seed(3)
+    E, H, I, G = 4, 64, 32, 32
+
+    def w4(n, k):
+        codes = torch.randint(-8, 8, (n, k), generator=g)
+        packed = ((codes[:, 0::2] & 0xF) | ((codes[:, 1::2] & 0xF) << 4)).to(torch.uint8)
+        return pkg.QTensor(packed, torch.rand(n, k // G, generator=g) * 0.02 + 1e-3,
+                           scheme="per_group_i4", group_size=G, codebook="int4")
+    experts = [(w4(2 * I, H), w4(H, I)) for _ in range(E)]
+    moe = pkg.SparseMoE(gate=torch.randn(E, H, generator=g) * 0.05, experts=experts, top_k=2)
+    assert not moe.grouped and len(moe.experts) == E
+    x = torch.randn(1, 5, H)
+    with torch.inference_mode():
+        y = moe(x)
+        topw, topi = moe.route(x.reshape(-1, H))
+        want = torch.zeros(5, H)
+        for e in range(E):
+            tok, slot = (topi == e).nonzero(as_tuple=True)
+            if tok.numel():
+                want.index_add_(0, tok, moe.experts[e](x.reshape(-1, H)[tok]) * topw[tok, slot, None])
+    assert torch.equal(y.reshape(5, H), want)
+
+
 def test_sparse_moe_group_limited_routing(pkg):
     """tests/test_deepseek.py:207-265: with 2 groups of 2 experts and topk_group=1,
     every token's experts come from one group."""

@@ -189,3 +189,36 @@ def test_w4a8_tile8_group256_bitexact(pkg, M, N, K):
     qt = _w4(pkg, N, K, 256, seed=M + N)
     bias = torch.randn(N, device="cuda").half()
     _check(pkg, _x(M, K, seed=M * 7 + K), qt, bias)
+
+
+@pytest.mark.parametrize("T", [3, 40])
+def test_sparse_moe_w4_experts_against_oracle(pkg, T):
+    """SparseMoE over per_group_i4 int4 experts (the reference builds experts
+    from any QTensor scheme, fni8serve/models/moe.py:56; its converter writes
+    per_group_i4 for weight_bits=4, convert.py:130-131): the layer output bit for
+    bit against the oracle's sort, per-expert W4A8 chain (gate_up, silu-and-mul,
+    down) and combine, on the same routing.  T = 3 leaves every expert below the
+    fused activation's row threshold, T = 40 puts several experts above it."""
+    E, H, I, k, G = 16, 512, 256, 4, 64
+    experts = [(_w4(pkg, 2 * I, H, G, seed=e), _w4(pkg, H, I, G, seed=100 + e)) for e in range(E)]
+    g = torch.Generator(device="cuda").manual_seed(T)
+    gate = (torch.randn(E, H, device="cuda", generator=g) * 0.05).half()
+    moe = pkg.SparseMoE(gate=gate, experts=experts, top_k=k, norm_topk_prob=True)
+    x = _x(T, H, seed=T + 7).reshape(1, T, H)
+    out = moe(x)
+    topw, topi = moe.route(x.reshape(-1, H))
+    torch.cuda.synchronize()
+    seg, rt, _, pos = o.moe_sort(topi.cpu().numpy(), E)
+    xf = x.reshape(-1, H).cpu().numpy()
+    ys = np.zeros((T * k, H), np.float16)
+    for e in range(E):
+        lo, hi = int(seg[e]), int(seg[e + 1])
+        if hi == lo:
+            continue
+        gu, dn = experts[e]
+        h, _, _ = o.linear_w4a8_f16(xf[rt[lo:hi]], gu.data.cpu().numpy(), gu.scale.cpu().numpy(), G)
+        a = o.act_and_mul_f16(h, "silu")
+        yd, _, _ = o.linear_w4a8_f16(a, dn.data.cpu().numpy(), dn.scale.cpu().numpy(), G)
+        ys[lo:hi] = yd
+    want = o.moe_combine_f16(ys, topi.cpu().numpy(), topw.cpu().numpy(), pos)
+    assert np.array_equal(out.reshape(T, H).cpu().numpy().view(np.uint16), want.view(np.uint16))
