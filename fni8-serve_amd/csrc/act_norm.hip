@@ -65,15 +65,10 @@ __device__ __forceinline__ uint4 act_chunk(uint4 g, uint4 u) {
     return make_uint4(o[0], o[1], o[2], o[3]);
 }
 
+// the running max of magnitude bits, as one 16-bit maximum
 __device__ __forceinline__ uint32_t chunk_amax(uint4 v, uint32_t amax) {
-    const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t lo = w4[i] & 0x7fffu, hi = (w4[i] >> 16) & 0x7fffu;
-        amax = lo > amax ? lo : amax;
-        amax = hi > amax ? hi : amax;
-    }
-    return amax;
+    const uint32_t m = fni8::amax_fold(fni8::amax_chunk(0u, v));
+    return m > amax ? m : amax;
 }
 
 // Row max over a workgroup of TPB threads (every thread gets it).

@@ -139,20 +139,72 @@ __device__ __forceinline__ uint32_t quant_fast(float x, float s, float yr) {
     return __builtin_bit_cast(uint32_t, v + 12582912.0f) & 0xffu;
 }
 
+// t = fl(h * yr) for the fp16 value in half HI of `packed`, as one v_fma_mix_f32
+// with a -0 addend: fma(h, yr, -0) rounds h * yr once and keeps the sign of a
+// zero product, so it is bitwise the product, without a separate f16 -> f32
+// conversion.
+template <int HI>
+__device__ __forceinline__ float mul_half(uint32_t packed, float yr) {
+    float t;
+    if constexpr (HI)
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+            : "=v"(t) : "v"(packed), "v"(yr), "v"(-0.0f));
+    else
+        asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[1,0,0]"
+            : "=v"(t) : "v"(packed), "v"(yr), "v"(-0.0f));
+    return t;
+}
+
+// quant_fast for half HI of `packed`; the low byte of the result is q (the
+// upper bytes hold the rounding constant and are discarded by the packing).
+template <int HI>
+__device__ __forceinline__ uint32_t quant_half(uint32_t packed, float s, float yr) {
+    const float x = h2f((uint16_t)(HI ? packed >> 16 : packed & 0xffffu));
+    const float t = mul_half<HI>(packed, yr);
+    const float r = __builtin_fmaf(-t, s, x);  // emitted as v_fma_mix_f32 on the fp16 x
+    const float v = __builtin_fmaf(r, yr, t);
+    return __builtin_bit_cast(uint32_t, v + 12582912.0f);
+}
+
+// Low bytes of four words -> one word (b0 | b1 << 8 | b2 << 16 | b3 << 24),
+// three byte permutes.
+__device__ __forceinline__ uint32_t pack_low_bytes(uint32_t b0, uint32_t b1, uint32_t b2,
+                                                   uint32_t b3) {
+    const uint32_t p01 = __builtin_amdgcn_perm(b1, b0, 0x0c0c0400u);
+    const uint32_t p23 = __builtin_amdgcn_perm(b3, b2, 0x0c0c0400u);
+    return __builtin_amdgcn_perm(p23, p01, 0x05040100u);
+}
+
 // 8 fp16 (one 16-byte chunk) -> 8 int8; zeros unless `live` (finite scale, real row).
+// About 4.75 VALU operations per element: two mixed-precision FMAs, one FMA,
+// one addition, and 3/4 of a byte permute.
 __device__ __forceinline__ uint2 quant_chunk(uint4 v, float s, float yr, bool live) {
     const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
     uint32_t out[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const uint32_t a = w4[2 * i], b = w4[2 * i + 1];
-        const uint32_t q0 = quant_fast(h2f((uint16_t)(a & 0xffffu)), s, yr);
-        const uint32_t q1 = quant_fast(h2f((uint16_t)(a >> 16)), s, yr);
-        const uint32_t q2 = quant_fast(h2f((uint16_t)(b & 0xffffu)), s, yr);
-        const uint32_t q3 = quant_fast(h2f((uint16_t)(b >> 16)), s, yr);
-        out[i] = live ? (q0 | (q1 << 8) | (q2 << 16) | (q3 << 24)) : 0u;
+        const uint32_t q = pack_low_bytes(quant_half<0>(a, s, yr), quant_half<1>(a, s, yr),
+                                          quant_half<0>(b, s, yr), quant_half<1>(b, s, yr));
+        out[i] = live ? q : 0u;
     }
     return make_uint2(out[0], out[1]);
+}
+
+// Running max of fp16 magnitude bits, two halves at a time: m holds two
+// 16-bit maxima (v_pk_max_u16 over (w & 0x7fff7fff)); amax_fold gives the row's.
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t amax_step(uint32_t m, uint32_t w) {
+    const u16x2 a = __builtin_bit_cast(u16x2, m);
+    const u16x2 b = __builtin_bit_cast(u16x2, w & 0x7fff7fffu);
+    return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+__device__ __forceinline__ uint32_t amax_chunk(uint32_t m, uint4 v) {
+    return amax_step(amax_step(amax_step(amax_step(m, v.x), v.y), v.z), v.w);
+}
+__device__ __forceinline__ uint32_t amax_fold(uint32_t m) {
+    const uint32_t lo = m & 0xffffu, hi = m >> 16;
+    return lo > hi ? lo : hi;
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {

@@ -109,16 +109,8 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
         for (int m = 0; m < MM; m++) {
             uint32_t am = 0;
 #pragma unroll
-            for (int i = 0; i < KCH; i++) {
-                const uint32_t w4[4] = {xr[m][i].x, xr[m][i].y, xr[m][i].z, xr[m][i].w};
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const uint32_t lo = w4[q] & 0x7fffu, hi = (w4[q] >> 16) & 0x7fffu;
-                    am = lo > am ? lo : am;
-                    am = hi > am ? hi : am;
-                }
-            }
-            am = fni8::wave_max_uniform(am);
+            for (int i = 0; i < KCH; i++) am = fni8::amax_chunk(am, xr[m][i]);
+            am = fni8::wave_max_uniform(fni8::amax_fold(am));
             if (lane == 0) amx[wave * MM + m] = am;
         }
         __syncthreads();

@@ -260,10 +260,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
                                 GROUPED ? rmap : nullptr, ws, bias, y, ldy, acc_out);
 }
 
-// ---- fp16 activations, M <= 4, quantized in the kernel ----------------------
+// ---- fp16 activations, M <= MM, quantized in the kernel --------------------
+// MM (4, 8 or 16): token rows of the int8 activation area; the MFMA A operand
+// has 16 rows, tokens past M repeat token M-1 (computed, never stored).
 // PQ: each wave's K share is 4*PQ slabs (K = 512 * WAVES * PQ exactly), which
 // makes every loop trip count a compile-time constant.
-template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB>
+// The lane's fp16 chunks stay in registers between the max and the quantize
+// pass when there are at most 16 of them (MM * PQ <= 16); otherwise the
+// quantize pass loads them again (from cache: the max pass just read them).
+template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, int MM = 4>
 __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int M, int K, const int8_t* __restrict__ w,
     const float* __restrict__ ws, int N, const uint16_t* __restrict__ bias,
@@ -271,14 +276,15 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     float* __restrict__ xs_out, int32_t* __restrict__ acc_out) {
     constexpr int ROWS = 16 * NB;
     constexpr int TILE = ROWS * 128;
-    constexpr int PER = 4 * PQ;           // slabs per wave
-    constexpr int NBT = PER / SB;         // batches per wave
-    constexpr int XAREA = PER * 4 * 128;  // the wave's int8 activations: [PER][4 tokens][128]
+    constexpr int PER = 4 * PQ;            // slabs per wave
+    constexpr int NBT = PER / SB;          // batches per wave
+    constexpr int XAREA = PER * MM * 128;  // the wave's int8 activations: [PER][MM tokens][128]
+    constexpr bool KEEP = MM * PQ <= 16;   // fp16 chunks kept in registers between passes
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
     int8_t* tiles = smem;                                     // [WAVES][SB][TILE]
     int8_t* xarea = smem + WAVES * SB * TILE;                 // [WAVES][XAREA]
-    uint32_t* amx = reinterpret_cast<uint32_t*>(xarea + WAVES * XAREA);  // [WAVES][4]
-    float* scl = reinterpret_cast<float*>(amx + WAVES * 4);   // [4]
+    uint32_t* amx = reinterpret_cast<uint32_t*>(xarea + WAVES * XAREA);  // [WAVES][MM]
+    float* scl = reinterpret_cast<float*>(amx + WAVES * MM);  // [MM]
     i32x4* red = reinterpret_cast<i32x4*>(smem);              // after the main loop
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -287,18 +293,20 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     const int s0 = wave * PER;
     const int r = lane & 15, g = lane >> 4;
 
-    // 1. activation loads first (the compiler then waits for them without
-    //    waiting for the weight loads issued after): chunk j of this lane is
-    //    token j / PQ, elements s0*128 + ((j % PQ) * 64 + lane) * 8 .. + 8.
-    uint4 xv[4 * PQ];
-#pragma unroll
-    for (int j = 0; j < 4 * PQ; j++) {
+    // chunk j of this lane: token j / PQ, elements s0*128 + ((j % PQ) * 64 + lane) * 8 .. + 8
+    auto xchunk = [&](int j) -> uint4 {
         const int m = j / PQ;
         if (m < M)
-            xv[j] = *reinterpret_cast<const uint4*>(
-                x + (int64_t)m * ldx + (int64_t)s0 * 128 + ((j % PQ) * 64 + lane) * 8);
-        else
-            xv[j] = make_uint4(0, 0, 0, 0);
+            return *reinterpret_cast<const uint4*>(x + (int64_t)m * ldx + (int64_t)s0 * 128 +
+                                                   ((j % PQ) * 64 + lane) * 8);
+        return make_uint4(0, 0, 0, 0);
+    };
+    // 1. activation loads first (the compiler then waits for them without
+    //    waiting for the weight loads issued after)
+    uint4 xv[KEEP ? MM * PQ : 1];
+    if constexpr (KEEP) {
+#pragma unroll
+        for (int j = 0; j < MM * PQ; j++) xv[j] = xchunk(j);
     }
     // 2. first weight batch
     WeightLanes<NB, RB> wl;
@@ -312,56 +320,44 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     // 3. row max magnitudes: integer max over (bits & 0x7fff), one wave-uniform
     //    value per token, then across the waves
 #pragma unroll
-    for (int m = 0; m < 4; m++) {
+    for (int m = 0; m < MM; m++) {
         uint32_t mx = 0;
 #pragma unroll
-        for (int jj = 0; jj < PQ; jj++) {
-            const uint4 v = xv[m * PQ + jj];
-            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t lo = w4[e] & 0x7fffu, hi = (w4[e] >> 16) & 0x7fffu;
-                mx = lo > mx ? lo : mx;
-                mx = hi > mx ? hi : mx;
-            }
-        }
-        mx = fni8::wave_max_uniform(mx);
-        if (lane == 0) amx[wave * 4 + m] = mx;
+        for (int jj = 0; jj < PQ; jj++) mx = fni8::amax_chunk(mx, KEEP ? xv[m * PQ + jj] : xchunk(m * PQ + jj));
+        mx = fni8::wave_max_uniform(fni8::amax_fold(mx));
+        if (lane == 0) amx[wave * MM + m] = mx;
     }
     lds_barrier();
-    float sc[4], yr[4];
-    bool live[4];
-#pragma unroll
-    for (int m = 0; m < 4; m++) {
-        uint32_t a = amx[m];
-#pragma unroll
-        for (int wv = 1; wv < WAVES; wv++) a = amx[wv * 4 + m] > a ? amx[wv * 4 + m] : a;
-        sc[m] = fni8::row_scale_from_bits(a);
-        live[m] = m < M && __builtin_isfinite(sc[m]);  // NaN/inf scale: every q is 0
-        yr[m] = 1.0f / sc[m];                          // correctly rounded (build flag)
-    }
-    if (wave == 0 && lane < 4) {
-        scl[lane] = lane == 0 ? sc[0] : lane == 1 ? sc[1] : lane == 2 ? sc[2] : sc[3];
-        if (blockIdx.x == 0 && lane < M) xs_out[lane] = scl[lane];
-    }
-    // 4. quantize this wave's share into its LDS area (token rows of 128 bytes
-    //    per slab; rows of different tokens are 128 bytes apart, so the A-operand
-    //    reads below are conflict-free without a swizzle)
+    // 4. quantize this wave's share into its LDS area: token rows of 128 bytes per
+    //    slab, 16-byte chunks swizzled by token (conflict-free A-operand reads)
     int8_t* xw = xarea + wave * XAREA;
 #pragma unroll
-    for (int j = 0; j < 4 * PQ; j++) {
-        const int m = j / PQ;
+    for (int m = 0; m < MM; m++) {
+        uint32_t a = amx[m];
+#pragma unroll
+        for (int wv = 1; wv < WAVES; wv++) a = amx[wv * MM + m] > a ? amx[wv * MM + m] : a;
+        const float sc = fni8::row_scale_from_bits(a);
+        const bool live = m < M && __builtin_isfinite(sc);  // NaN/inf scale: every q is 0
+        const float yr = 1.0f / sc;                          // correctly rounded (build flag)
+        if (wave == 0 && lane == 0) {
+            scl[m] = sc;
+            if (blockIdx.x == 0 && m < M) xs_out[m] = sc;
+        }
         if (m >= M) continue;
-        const int kl = ((j % PQ) * 64 + lane) * 8;  // element offset in the share
-        const uint2 q = fni8::quant_chunk(xv[j], sc[m], yr[m], live[m]);
-        *reinterpret_cast<uint2*>(xw + ((kl >> 7) * 4 + m) * 128 + (kl & 127)) = q;
-        if (blockIdx.x == 0)
-            *reinterpret_cast<uint2*>(xq_out + (int64_t)m * K + (int64_t)s0 * 128 + kl) = q;
+#pragma unroll
+        for (int jj = 0; jj < PQ; jj++) {
+            const int kl = (jj * 64 + lane) * 8;  // element offset in the share
+            const uint2 q = fni8::quant_chunk(KEEP ? xv[m * PQ + jj] : xchunk(m * PQ + jj), sc, yr, live);
+            *reinterpret_cast<uint2*>(xw + ((kl >> 7) * MM + m) * 128 + swz(m, (kl & 127) >> 4) +
+                                      (kl & 15)) = q;
+            if (blockIdx.x == 0)
+                *reinterpret_cast<uint2*>(xq_out + (int64_t)m * K + (int64_t)s0 * 128 + kl) = q;
+        }
     }
     const int tok = r < M ? r : M - 1;  // tokens past M repeat M-1 (never stored)
     int aoff[2];
 #pragma unroll
-    for (int q = 0; q < 2; q++) aoff[q] = tok * 128 + q * 64 + g * 16;
+    for (int q = 0; q < 2; q++) aoff[q] = tok * 128 + swz(tok, 4 * q + g);
 
     // 5. the weight stream
     i32x4 acc[2][1][NB];
@@ -381,7 +377,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
         asm volatile("" ::: "memory");
 #pragma unroll
         for (int j = 0; j < SB; j++) {
-            const int8_t* xs_ = xw + (bt * SB + j) * 512;
+            const int8_t* xs_ = xw + (bt * SB + j) * (MM * 128);
             const i32x4 a0 = ld16(xs_ + aoff[0]), a1 = ld16(xs_ + aoff[1]);
             i32x4 bf[NB][2];
 #pragma unroll
@@ -443,25 +439,29 @@ int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const i
     return FNI8_OK;
 }
 
-template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB>
+template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, int MM = 4>
 int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, const float* ws,
                  int N, const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
                  float* xs_out, int32_t* acc_out, hipStream_t st) {
     static_assert((4 * PQ) % SB == 0, "batches must divide the share");
-    if (K != 512 * WAVES * PQ) return 1;
+    static_assert(MM == 4 || MM == 8 || MM == 16, "token rows of the activation area");
+    if (K != 512 * WAVES * PQ || M > MM) return 1;
     constexpr size_t tiles = (size_t)WAVES * SB * 16 * NB * 128;
-    const size_t lds_main = tiles + (size_t)WAVES * 4 * PQ * 512 + WAVES * 16 + 16;
+    constexpr size_t lds_main = tiles + (size_t)WAVES * MM * PQ * 512 + WAVES * MM * 4 + MM * 4;
     constexpr size_t red = (size_t)WAVES * NB * 64 * 16;
-    const size_t lds = lds_main > red ? lds_main : red;
-    if (lds > 160 * 1024) return 1;
-    auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ, RB>;
-    static const bool ok = hipFuncSetAttribute((const void*)kern,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               160 * 1024) == hipSuccess;
-    if (!ok) return 1;
-    hipLaunchKernelGGL(kern, dim3((unsigned)((N + 8 * RB - 1) / (8 * RB))), dim3(WAVES * 64), lds,
-                       st, x, ldx, M, K, w, ws, N, bias, y, ldy, xq_out, xs_out, acc_out);
-    return FNI8_OK;
+    constexpr size_t lds = lds_main > red ? lds_main : red;
+    if constexpr (lds > 160 * 1024) {
+        return 1;
+    } else {
+        auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ, RB, MM>;
+        static const bool ok = hipFuncSetAttribute((const void*)kern,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   160 * 1024) == hipSuccess;
+        if (!ok) return 1;
+        hipLaunchKernelGGL(kern, dim3((unsigned)((N + 8 * RB - 1) / (8 * RB))), dim3(WAVES * 64),
+                           lds, st, x, ldx, M, K, w, ws, N, bias, y, ldy, xq_out, xs_out, acc_out);
+        return FNI8_OK;
+    }
 }
 
 // True when 24-row workgroups fill the CUs better than 32-row ones in whole

@@ -1,8 +1,9 @@
 // Prefill GEMM, "ping-pong" form (gfx950, v_mfma_i32_32x32x32_i8).
 //
 // Workgroup: 8 waves in two groups of four (one wave of each group per SIMD).
-// Wave (g, s) owns rows g*BM/2.. and columns s*BN/4.. of the BM x BN macro tile:
-// FM = BM/64 by FN = BN/128 blocks of 32x32 int32 accumulators.  The groups take
+// Group g owns rows g*BM/2.. of the BM x BN macro tile; inside it wave s owns
+// BM/2 rows x BN/4 columns (tiles 256x256, 128x256, 256x128), or BM/4 x BN/2 for
+// the 256x192 tile, as 32x32 blocks of int32 accumulators.  The groups take
 // turns: while one group issues its MFMAs for a 64-byte K unit, the other reads
 // its operand fragments for the same unit from LDS and issues the global->LDS
 // copies, then they swap at a workgroup barrier.  Each SIMD thus always has one
@@ -56,7 +57,9 @@ __device__ __forceinline__ void slot_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int BM, int BN, bool WRITE_ACC>
+// WC: waves of a group along N (4: a wave owns BM/2 rows x BN/4 columns; 2: a
+// wave owns BM/4 x BN/2, for BN = 192 where BN/4 is not a multiple of 32).
+template <int BM, int BN, bool WRITE_ACC, int WC = 4>
 __global__ __launch_bounds__(512) void gemm_pp_kernel(
     const int8_t* __restrict__ aq, int64_t lda, const float* __restrict__ as, int M, int K,
     const int8_t* __restrict__ w, const float* __restrict__ ws, int N,
@@ -66,13 +69,18 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     constexpr int STAGE = (BM + BN) * BK;    // bytes per LDS stage (two stages)
     constexpr int D = STAGE / 8192;          // copy instructions per wave per k-tile
     constexpr int AINS = BM * CPR / 64;      // the first AINS instructions of a stage cover A
-    constexpr int FM = BM / 64, FN = BN / 128;
+    constexpr int WR = 4 / WC;                           // waves of a group along M
+    constexpr int FM = BM / (64 * WR), FN = BN / (32 * WC);
+    static_assert(WC == 4 || WC == 2, "wave arrangement inside a group");
+    static_assert(FM * 64 * WR == BM && FN * 32 * WC == BN, "whole 32x32 blocks per wave");
     static_assert(D * 8192 == STAGE, "a stage must split evenly over the 8 waves");
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = wave >> 2, s = wave & 3;
+    const int wrow = g * (BM / 2) + (s / WC) * (FM * 32);  // first row of the wave's blocks
+    const int wcol = (s % WC) * (FN * 32);                 // first column
 
     int m0, m1, n0;
     fni8t::dense_tile<BM, BN>(M, N, m0, m1, n0);
@@ -160,11 +168,11 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
 #pragma unroll
                     for (int i = 0; i < FM; i++)
                         af[ks][i] = *reinterpret_cast<const i32x4*>(
-                            sb + (g * (BM / 2) + i * 32) * BK + loff[h * 2 + ks]);
+                            sb + (wrow + i * 32) * BK + loff[h * 2 + ks]);
 #pragma unroll
                     for (int j = 0; j < FN; j++)
                         bf[ks][j] = *reinterpret_cast<const i32x4*>(
-                            sb + BM * BK + (s * (BN / 4) + j * 32) * BK + loff[h * 2 + ks]);
+                            sb + BM * BK + (wcol + j * 32) * BK + loff[h * 2 + ks]);
                 }
                 // fragments in registers before the slot ends: once every wave
                 // has passed the barrier the stage may be refilled
@@ -192,11 +200,12 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     if (g == 0) slot_barrier();
     __syncthreads();  // every copy has landed and every wave is done with the stages
 
-    fni8t::tile_epilogue<BM, BN, false, WRITE_ACC>(acc, smem, tid, lane, g, s, m0, m1, n0, N,
-                                                   nullptr, as, ws, bias, y, ldy, acc_out);
+    fni8t::tile_epilogue<BM, BN, false, WRITE_ACC, FM, FN>(
+        acc, smem, tid, lane, g, wrow - g * (BM / 2), wcol, m0, m1, n0, N, nullptr, as, ws, bias,
+        y, ldy, acc_out);
 }
 
-template <int BM, int BN>
+template <int BM, int BN, int WC = 4>
 int launch(const int8_t* aq, int64_t lda, const float* as, int M, int K, const int8_t* w,
            const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
            int32_t* acc_out, hipStream_t st) {
@@ -209,7 +218,7 @@ int launch(const int8_t* aq, int64_t lda, const float* as, int M, int K, const i
     // (a repeated set with the same value is harmless).
     auto run = [&](auto acc_c) -> int {
         constexpr bool ACC = decltype(acc_c)::value;
-        const auto kern = gemm_pp_kernel<BM, BN, ACC>;
+        const auto kern = gemm_pp_kernel<BM, BN, ACC, WC>;
         static bool attr_set = false;
         if (!attr_set) {
             hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -246,9 +255,16 @@ namespace fni8h {
 
 // Returns 1 when the shape is not taken (the caller falls back), else an FNI8 code.
 // Dense only; needs K % 128 == 0 and 16-byte aligned operand rows.  Tiles: the
-// shape from {256x256, 128x256, 256x128} with the least estimated time, counting
-// whole rounds of one workgroup per CU and the lower MFMA rate of the smaller
-// tiles (each of their k-tiles moves 3/4 of the bytes for 1/2 of the products).
+// shape from {256x256, 256x192, 128x256, 256x128} with the least estimated
+// time, counting whole rounds of one workgroup per CU and each tile's time
+// relative to 256x256, measured on MI355X over the Qwen3-8B prefill GEMMs:
+// 256x192 takes 0.79 of it for 0.75 of the products (the 2x2 wave arrangement
+// reads 5 fragments per 6 MFMAs instead of 6 per 8), the half-size tiles about
+// 2/3 (each of their k-tiles moves 3/4 of the bytes for 1/2 of the products).
+// QKV (N = 6144) at M = 4096 is the case 256x192 exists for: 512 tiles make two
+// full rounds on 256 CUs where 256x256 leaves the second round half empty
+// (117 -> 103 us).  Between the two half-size tiles, long K (down, K = 12288)
+// runs 256x128 4% faster and short K 128x256 3% faster.
 // Expert segments stay on the 32x32x32 tile kernel: the MoE projections have
 // short K (768 and 2048 bytes, 6 and 16 k-tiles), where a grouped form of this
 // kernel (128x256 segment tiles) measured 18% slower at T = 4096 (473 against
@@ -261,28 +277,31 @@ int launch_pp(const int8_t* aq, int64_t lda, const float* as, int64_t M, int64_t
     if (256 * K >= ((int64_t)1 << 32) || 256 * lda >= ((int64_t)1 << 32)) return 1;
     const int m = (int)M, k = (int)K, n = (int)N;
     const int cus = cu_count();
-    constexpr int kTiles[3][2] = {{256, 256}, {128, 256}, {256, 128}};
-    constexpr double kCost[3] = {1.0, 0.5 / 0.75, 0.5 / 0.75};   // relative time of one tile
+    const bool longk = K >= 8192;
+    // candidates in order of preference on equal estimates
+    const int kTiles[4][2] = {{256, 256}, {256, 192}, {longk ? 256 : 128, longk ? 128 : 256},
+                              {longk ? 128 : 256, longk ? 256 : 128}};
+    constexpr double kCost[4] = {1.0, 0.79, 0.5 / 0.75, 0.5 / 0.75};  // time of one tile
     int best = 0;
     double best_t = 1e30;
-    for (int i = 0; i < 3; i++) {
+    int64_t best_wgs = 0;
+    for (int i = 0; i < 4; i++) {
         const int64_t wgs = ((M + kTiles[i][0] - 1) / kTiles[i][0]) * ((N + kTiles[i][1] - 1) / kTiles[i][1]);
         const double tm = (double)((wgs + cus - 1) / cus) * kCost[i];
         if (tm < best_t - 1e-9) {
             best_t = tm;
             best = i;
+            best_wgs = wgs;
         }
     }
-    // Too few workgroups for these tiles (prefill M = 512): the caller's
-    // smaller-tile kernel fills the CUs better.
-    const int64_t wgs = ((M + kTiles[best][0] - 1) / kTiles[best][0]) *
-                        ((N + kTiles[best][1] - 1) / kTiles[best][1]);
-    if (4 * wgs < 3 * (int64_t)cus) return 1;
-    switch (best) {
-        case 0: return launch<256, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
-        case 1: return launch<128, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
-        default: return launch<256, 128>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
-    }
+    // Too few workgroups for these tiles (prefill M = 512 except gate_up): the
+    // caller's smaller-tile kernel fills the CUs better.
+    if (4 * best_wgs < 3 * (int64_t)cus) return 1;
+    const int bm = kTiles[best][0], bn = kTiles[best][1];
+    if (bn == 192) return launch<256, 192, 2>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
+    if (bm == 256 && bn == 256) return launch<256, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
+    if (bm == 128) return launch<128, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
+    return launch<256, 128>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
 }
 
 }  // namespace fni8h

@@ -172,8 +172,8 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
     compute(C1{});
     __syncthreads();  // every wave is done with the LDS stages
 
-    tile_epilogue<BM, BN, GROUPED, WRITE_ACC>(acc, smem, tid, lane, wm, wn, m0, m1, n0, N,
-                                              row_index, as, wsexp, bexp, y, ldy, acc_out);
+    tile_epilogue<BM, BN, GROUPED, WRITE_ACC>(acc, smem, tid, lane, wm, 0, wn * (BN / 4), m0, m1,
+                                              n0, N, row_index, as, wsexp, bexp, y, ldy, acc_out);
 }
 
 template <int BM, int BN, int BK, bool GROUPED>

@@ -31,15 +31,9 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rowwise_regs_kernel(
     for (int c = 0; c < CH; c++) {
         const int k = (c * kQuantThreads + tid) * 8;
         v[c] = k < K ? *reinterpret_cast<const uint4*>(xr + k) : make_uint4(0, 0, 0, 0);
-        const uint32_t w4[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t lo = w4[i] & 0x7fffu, hi = (w4[i] >> 16) & 0x7fffu;
-            amax = lo > amax ? lo : amax;
-            amax = hi > amax ? hi : amax;
-        }
+        amax = fni8::amax_chunk(amax, v[c]);
     }
-    amax = fni8::wave_max_uniform(amax);
+    amax = fni8::wave_max_uniform(fni8::amax_fold(amax));
     if ((tid & 63) == 0) red[tid >> 6] = amax;
     __syncthreads();
     amax = red[0];

@@ -42,16 +42,18 @@ constexpr size_t tile_epilogue_lds() {
 // scale and writes 8 contiguous bytes per lane.  Column scales and the bias
 // (converted to fp32 once, which is exact) are staged in LDS and read four at a
 // time.  The caller has finished with its LDS stages (a barrier before the call).
+// wm: the wave's half of the tile (rows wm*BM/2..); roff, coff: the row (inside
+// that half) and column of the wave's first 32x32 block.
 template <int BM, int BN, bool GROUPED, bool WRITE_ACC, int FM = BM / 64, int FN = BN / 128>
 __device__ __forceinline__ void tile_epilogue(const i32x16 (&acc)[FM][FN], int8_t* smem, int tid,
-                                              int lane, int wm, int wn, int m0, int m1, int n0,
+                                              int lane, int wm, int roff, int coff, int m0, int m1, int n0,
                                               int N, const int32_t* __restrict__ row_index,
                                               const float* __restrict__ as,
                                               const float* __restrict__ wsexp,
                                               const uint16_t* __restrict__ bexp,
                                               uint16_t* __restrict__ y, int64_t ldy,
                                               int32_t* __restrict__ acc_out) {
-    constexpr int NT = 512, WTN = BN / 4;
+    constexpr int NT = 512;
     constexpr int HALF = BM / 2;          // rows staged per pass (one wave-row)
     constexpr int OTS = BN + 8;           // int32 row stride of the staging tile
     float* as_l = reinterpret_cast<float*>(smem);
@@ -81,8 +83,8 @@ __device__ __forceinline__ void tile_epilogue(const i32x16 (&acc)[FM][FN], int8_
                 for (int j = 0; j < FN; j++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) {
-                        const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        const int col = wn * WTN + j * 32 + (lane & 31);
+                        const int row = roff + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        const int col = coff + j * 32 + (lane & 31);
                         ot[row * OTS + col] = acc[i][j][r];
                     }
         }

@@ -165,6 +165,29 @@ def test_prefill_bias_shipped_kernel(pkg, wl, cuda):
     assert np.array_equal(_f16bits(y), yr.view(np.uint16))
 
 
+@pytest.mark.parametrize("want_acc", [False, True])
+def test_prefill_tile_192_ragged(pkg, wl, cuda, want_acc):
+    """The 256x192 prefill tile (chosen when it fills the CUs in fewer
+    tile-rounds) with a partial last row tile (2000 = 7*256 + 208) and a
+    partial last column tile (6080 = 31*192 + 128), with bias; both kernel
+    instantiations (with and without the accumulator output), sampled rows
+    including the last ones, against the oracle bit for bit."""
+    M, N, K = 2000, 6080, 1024
+    x = wl.activations(M, K, seed=61)
+    q, s = wl.weight_i8(N, K, seed=62)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(63)) * 2).half()
+    qt = pkg.QTensor(q.cuda(), s.cuda(), scheme="per_row_i8")
+    y, xq, xs, acc = pkg.linear_with_intermediates(x.cuda(), qt, bias.cuda(), want_acc=want_acc)
+    torch.cuda.synchronize()
+    xqr, xsr = oracle.quant_rowwise_f16(x.numpy())
+    rows = np.unique(np.concatenate([_sample_rows(M, 64), np.arange(M - 50, M)]))
+    accr = oracle.gemm_i8(xqr[rows], q.numpy())
+    if want_acc:
+        assert np.array_equal(acc.cpu().numpy()[rows], accr), "int32 accumulators differ"
+    yr = oracle.dequant_f16(accr, xsr[rows], s.numpy(), bias.numpy())
+    assert np.array_equal(_f16bits(y)[rows], yr.view(np.uint16)), "fp16 outputs differ"
+
+
 def test_quant_exhaustive_fp16(pkg, cuda):
     """Every fp16 bit pattern, in rows of 1024 (rows with inf/NaN get an inf/NaN
     scale), plus the same values under one fixed large scale."""
