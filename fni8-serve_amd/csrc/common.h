@@ -272,6 +272,70 @@ __device__ __forceinline__ bool find_group_tile(const int32_t* __restrict__ seg_
     return false;
 }
 
+// Grouped GEMM work lookup in XCD order.  The work is every (expert e, n-tile
+// j, row tile r of e's segment), listed expert by expert, n-tile by n-tile,
+// row tile fastest: the row tiles that share one expert's weight tile are
+// neighbours, and one expert's n-tiles share its activation rows.  Workgroup i
+// of a 1-D grid runs on XCD i % 8 (the round-robin dispatch over the eight
+// XCDs), so item = remap(i) gives XCD x the contiguous run of items
+// [x*q + min(x, rem), ...) (q = W / 8, rem = W % 8 for W items): an expert's
+// weight and activation tiles are fetched into that XCD's L2 once and reused
+// there, instead of by up to eight L2s.  The remap is a bijection on [0, W),
+// so the result does not depend on the dispatch.  W is bounded by the grid (a
+// seg_off beyond the launch's bound loses its last items) and rows as in
+// find_group_tile.  Every lane of the wave gets the same answer; false past
+// the last item.
+__device__ __forceinline__ bool find_group_item(const int32_t* __restrict__ seg_off, int E,
+                                                int bm, int ntn, int rows, int& e_out,
+                                                int& r0, int& r1, int& j_out) {
+    const int lane = threadIdx.x & 63;
+    auto tiles_of = [&](int e, int& lo, int& hi) {
+        lo = 0;
+        hi = 0;
+        if (e < E) {
+            lo = seg_off[e];
+            hi = seg_off[e + 1];
+        }
+        return hi > lo ? (hi - lo + bm - 1) / bm : 0;
+    };
+    int W = 0;
+    for (int c = 0; c < E; c += 64) {
+        int lo, hi;
+        W += wave_sum_i32(tiles_of(c + lane, lo, hi));
+    }
+    W *= ntn;
+    W = W < (int)gridDim.x ? W : (int)gridDim.x;
+    const int i = blockIdx.x;
+    if (i >= W) return false;
+    const int q = W >> 3, rem = W & 7, x = i & 7;
+    const int item = x * q + (x < rem ? x : rem) + (i >> 3);
+    int base = 0;
+    for (int c = 0; c < E; c += 64) {
+        const int e = c + lane;
+        int lo, hi;
+        const int tiles = tiles_of(e, lo, hi);
+        const int items = tiles * ntn;
+        const int incl = wave_incl_scan_i32(items, lane);
+        const int excl = incl - items;
+        const bool mine = (e < E) && items > 0 && (item >= base + excl) && (item < base + incl);
+        const unsigned long long bal = __ballot(mine);
+        if (bal) {
+            const int src = __builtin_ctzll(bal);
+            const int lo_s = __shfl(lo, src, 64), hi_s = __shfl(hi, src, 64);
+            const int t_s = __shfl(tiles, src, 64);
+            const int local = item - base - __shfl(excl, src, 64);
+            e_out = __shfl(e, src, 64);
+            j_out = local / t_s;
+            r0 = lo_s + (local % t_s) * bm;
+            r1 = r0 + bm < hi_s ? r0 + bm : hi_s;
+            r1 = r1 < rows ? r1 : rows;
+            return r0 >= 0 && r0 < r1;
+        }
+        base += __shfl(incl, 63, 64);
+    }
+    return false;
+}
+
 }  // namespace fni8
 
 // Host-side launch helpers shared by the translation units.

@@ -63,10 +63,10 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
     const int8_t* wexp = w;
     const float* wsexp = ws;
     const uint16_t* bexp = bias;
-    if constexpr (GROUPED) {  // x = segment tile slot, y = n-tile
-        n0 = blockIdx.y * BN;
-        int e;
-        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, M, e, m0, m1)) return;
+    if constexpr (GROUPED) {  // one work item (expert, n-tile, row tile) per workgroup
+        int e, j;
+        if (!fni8::find_group_item(seg_off, E, BM, (N + BN - 1) / BN, M, e, m0, m1, j)) return;
+        n0 = j * BN;
         wexp += (int64_t)e * N * K;
         wsexp += (int64_t)e * N;
         if (bias) bexp += (int64_t)e * N;
@@ -186,7 +186,8 @@ int launch(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_in
     constexpr size_t lds = main_lds > epi_lds ? main_lds : epi_lds;
     static_assert(lds <= 160 * 1024, "LDS budget");
     const unsigned ntn = (unsigned)((N + BN - 1) / BN);
-    dim3 grid = GROUPED ? dim3(slots, ntn) : dim3(ntn * (unsigned)((M + BM - 1) / BM));
+    // grouped: an upper bound of the work items (slots row tiles per n-tile)
+    dim3 grid = GROUPED ? dim3(slots * ntn) : dim3(ntn * (unsigned)((M + BM - 1) / BM));
     // The LDS limit is a per-function attribute, so each instantiation (with and
     // without the accumulator output) is set once, by its own flag; setting it
     // again with the same value is idempotent, so a race between threads is harmless.

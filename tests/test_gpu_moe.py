@@ -123,9 +123,12 @@ _SPARSE = [0, 1, 0, 0, 33, 0, 2, 0, 0, 0, 0, 17, 0, 0, 0, 0, 0, 1, 0, 0, 0, 0, 0
     # <= 40 rows/expert: the tile kernel over 64-row segment tiles
     ([0, 70, 1, 17, 33, 0, 2, 4], 1536, 2048),   # ~16 rows/expert, a 2-tile segment
     ([40, 0, 64, 65, 1, 30, 48, 63], 104, 1024),  # ~39 rows/expert, N % 128 != 0
-    # > 40 rows/expert: the tile kernel over 128-row tiles, partial last tiles
+    # > 40 rows/expert: the tile kernel over 128-row tiles, partial last tiles,
+    # work items in XCD order (segments of 0 to 1000 rows, 1 to 12 n-tiles)
     ([0, 1, 63, 64, 65, 127, 128, 129, 191, 192, 255, 256, 300, 700], 264, 768),
     ([129, 0, 383, 64, 2, 256], 512, 2048),
+    ([256, 0, 255, 257, 512, 513, 1000, 1], 1536, 512),
+    ([600, 3, 300], 384, 256),
     ([0, 1, 63, 64, 65, 127, 128, 129, 300], 200, 640),  # K % 256 != 0: 64-byte K steps
 ])
 @pytest.mark.parametrize("gather", [False, True])
