@@ -289,49 +289,81 @@ __device__ __forceinline__ bool find_group_item(const int32_t* __restrict__ seg_
                                                 int bm, int ntn, int rows, int& e_out,
                                                 int& r0, int& r1, int& j_out) {
     const int lane = threadIdx.x & 63;
-    auto tiles_of = [&](int e, int& lo, int& hi) {
-        lo = 0;
-        hi = 0;
-        if (e < E) {
-            lo = seg_off[e];
-            hi = seg_off[e + 1];
-        }
-        return hi > lo ? (hi - lo + bm - 1) / bm : 0;
-    };
+    // One pass of loads: up to 4 chunks of 64 experts (E <= 256) stay in
+    // registers for the search, so the search needs no second round trip.
+    constexpr int CH = 4;
+    int lo[CH], hi[CH], items[CH], incl[CH], cbase[CH];
     int W = 0;
-    for (int c = 0; c < E; c += 64) {
-        int lo, hi;
-        W += wave_sum_i32(tiles_of(c + lane, lo, hi));
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int e = c * 64 + lane;
+        lo[c] = 0;
+        hi[c] = 0;
+        if (e < E) {
+            lo[c] = seg_off[e];
+            hi[c] = seg_off[e + 1];
+        }
+        const int tiles = hi[c] > lo[c] ? (hi[c] - lo[c] + bm - 1) / bm : 0;
+        items[c] = tiles * ntn;
+        incl[c] = wave_incl_scan_i32(items[c], lane);
+        cbase[c] = W;
+        W += __shfl(incl[c], 63, 64);
     }
-    W *= ntn;
+    for (int c = CH * 64; c < E; c += 64) {  // E > 256: the rest, counted only
+        const int e = c + lane;
+        int t = 0;
+        if (e < E) {
+            const int l = seg_off[e], h = seg_off[e + 1];
+            t = h > l ? (h - l + bm - 1) / bm : 0;
+        }
+        W += wave_sum_i32(t) * ntn;
+    }
     W = W < (int)gridDim.x ? W : (int)gridDim.x;
     const int i = blockIdx.x;
     if (i >= W) return false;
     const int q = W >> 3, rem = W & 7, x = i & 7;
     const int item = x * q + (x < rem ? x : rem) + (i >> 3);
-    int base = 0;
-    for (int c = 0; c < E; c += 64) {
-        const int e = c + lane;
-        int lo, hi;
-        const int tiles = tiles_of(e, lo, hi);
-        const int items = tiles * ntn;
-        const int incl = wave_incl_scan_i32(items, lane);
-        const int excl = incl - items;
-        const bool mine = (e < E) && items > 0 && (item >= base + excl) && (item < base + incl);
+    auto take = [&](int e, int l, int h, int its, int ex, int base) {
+        const int tiles = its / ntn;
+        const int local = item - base - ex;
+        e_out = e;
+        j_out = local / tiles;
+        r0 = l + (local % tiles) * bm;
+        r1 = r0 + bm < h ? r0 + bm : h;
+        r1 = r1 < rows ? r1 : rows;
+        return r0 >= 0 && r0 < r1;
+    };
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int excl = incl[c] - items[c];
+        const bool mine = (c * 64 + lane < E) && (item >= cbase[c] + excl) &&
+                          (item < cbase[c] + incl[c]);
         const unsigned long long bal = __ballot(mine);
         if (bal) {
             const int src = __builtin_ctzll(bal);
-            const int lo_s = __shfl(lo, src, 64), hi_s = __shfl(hi, src, 64);
-            const int t_s = __shfl(tiles, src, 64);
-            const int local = item - base - __shfl(excl, src, 64);
-            e_out = __shfl(e, src, 64);
-            j_out = local / t_s;
-            r0 = lo_s + (local % t_s) * bm;
-            r1 = r0 + bm < hi_s ? r0 + bm : hi_s;
-            r1 = r1 < rows ? r1 : rows;
-            return r0 >= 0 && r0 < r1;
+            return take(c * 64 + src, __shfl(lo[c], src, 64), __shfl(hi[c], src, 64),
+                        __shfl(items[c], src, 64), __shfl(excl, src, 64), cbase[c]);
         }
-        base += __shfl(incl, 63, 64);
+    }
+    int base = cbase[CH - 1] + __shfl(incl[CH - 1], 63, 64);
+    for (int c = CH * 64; c < E; c += 64) {
+        const int e = c + lane;
+        int l = 0, h = 0;
+        if (e < E) {
+            l = seg_off[e];
+            h = seg_off[e + 1];
+        }
+        const int its = (h > l ? (h - l + bm - 1) / bm : 0) * ntn;
+        const int inc = wave_incl_scan_i32(its, lane);
+        const int excl = inc - its;
+        const bool mine = (e < E) && (item >= base + excl) && (item < base + inc);
+        const unsigned long long bal = __ballot(mine);
+        if (bal) {
+            const int src = __builtin_ctzll(bal);
+            return take(c + src, __shfl(l, src, 64), __shfl(h, src, 64), __shfl(its, src, 64),
+                        __shfl(excl, src, 64), base);
+        }
+        base += __shfl(inc, 63, 64);
     }
     return false;
 }
