@@ -298,16 +298,26 @@ def prefill_roofline(wl, prefill, M=4096):
 
 
 def prefill_one(pkg, wl, pool, device, name, M, reps=8):
-    """One prefill shape only (for per-shape profiler runs): `reps` linear() calls
-    over the pool's layers, after one warm call."""
+    """One prefill shape only (for per-shape profiler runs), timed exactly as the
+    prefill section times it: the GEMM launch alone and the quantize launch
+    alone, each as three sleep-backed bursts (one warm call, then `reps` calls
+    over the pool's layers); the best burst's mean is reported, so a kernel
+    trace of this run reproduces the section's figures from its own dispatches
+    (per GEMM burst: 1 + reps dispatches, the last `reps` timed)."""
     N, K = wl.QWEN3_8B_LINEARS[name]
     x = wl.activations(M, K, seed=300 + M, device="cpu").to(device)
-    pkg.linear(x, pool[0][name])
-    torch.cuda.synchronize()
-    for i in range(reps):
-        pkg.linear(x, pool[(i + 1) % len(pool)][name])
-    torch.cuda.synchronize()
-    return {"shape": name, "M": M, "N": N, "K": K, "calls": reps + 1}
+    xq, xs = pkg.quantize_rowwise(x)
+    idx = [0]
+
+    def gemm():
+        qt = pool[idx[0] % len(pool)][name]
+        idx[0] += 1
+        pkg.gemm_w8a8(xq, xs, qt)
+
+    tg = min(time_burst(gemm, reps=reps) for _ in range(3))
+    tq = min(time_burst(lambda: pkg.quantize_rowwise(x), reps=reps) for _ in range(3))
+    return {"shape": name, "M": M, "N": N, "K": K, "bursts": 3, "reps": reps,
+            "gemm_us": round(tg * 1e6, 2), "quant_us": round(tq * 1e6, 2)}
 
 
 def moe_section(pkg, wl, device, ts=(16, 256, 4096)):
