@@ -156,6 +156,33 @@ def test_grouped_mfma_segments_bitexact(pkg, wl, cuda, sizes, N, K, gather):
     assert np.array_equal(y.cpu().numpy().view(np.uint16), yr.view(np.uint16))
 
 
+@pytest.mark.parametrize("E,mean_rows,N,K", [(300, 60, 256, 512), (260, 12, 200, 1024)])
+def test_grouped_many_experts_bitexact(pkg, wl, cuda, E, mean_rows, N, K):
+    """More than 256 experts: the work-item lookup keeps the first 256 experts'
+    offsets in registers and scans the rest in a second loop; items in both parts
+    (128-row tiles at ~60 rows per expert, 64-row tiles at ~12), with empty
+    experts, against the oracle bit for bit."""
+    rng = np.random.default_rng(E + K)
+    sizes = rng.integers(0, 2 * mean_rows, E)
+    sizes[rng.choice(E, E // 5, replace=False)] = 0
+    sizes[-1] = 2 * mean_rows + 3   # the last expert (second loop) is never empty
+    seg_r = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    R = int(seg_r[-1])
+    w, ws = wl.expert_weights(E, N, K, seed=E + 5)
+    A = R // 2 + 7
+    x = wl.activations(A, K, seed=E + 6)
+    aq, as_ = pkg.quantize_rowwise(x.cuda())
+    ri = rng.integers(0, A, R).astype(np.int32)
+    y, acc = pkg.gemm_w8a8_grouped(aq, as_, w.cuda(), ws.cuda(), torch.from_numpy(seg_r).cuda(), R,
+                                   row_index=torch.from_numpy(ri).cuda(), want_acc=True)
+    torch.cuda.synchronize()
+    aq_r, as_r = oracle.quant_rowwise_f16(x.numpy())
+    yr, accr = oracle.grouped_w8a8_f16(aq_r, as_r, w.numpy(), ws.numpy(), seg_r, row_index=ri,
+                                       want_acc=True)
+    assert np.array_equal(acc.cpu().numpy(), accr)
+    assert np.array_equal(y.cpu().numpy().view(np.uint16), yr.view(np.uint16))
+
+
 @pytest.mark.parametrize("T", [16, 256])
 def test_combine_bitexact(pkg, wl, cuda, T):
     E, k, H = wl.MOE["experts"], wl.MOE["top_k"], wl.MOE["hidden"]
