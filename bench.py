@@ -190,7 +190,25 @@ def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
         "frac_by_M": {f"M{m}": round(b / t / 1e9 / HBM_PEAK_GBS, 4) for m, (b, t) in by_m.items()},
         "per_shape_GBps": {k: round(b / t / 1e9, 1) for k, (b, t, n) in per.items()},
         "per_shape_us": {k: round(t / n * 1e6, 2) for k, (b, t, n) in per.items()},
+        "launch_floor_us": launch_floor_us(),
     }
+
+
+def launch_floor_us(reps=200):
+    """Time per launch of back-to-back empty kernels (torch's GPU sleep with a
+    zero count) behind a GPU-side sleep, HIP events on the launch stream: the
+    fixed cost every decode linear pays once (M <= 4) or twice (quantize +
+    GEMM above), whatever it streams."""
+    torch.cuda._sleep(0)
+    torch.cuda.synchronize()
+    torch.cuda._sleep(int(2.0e7))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        torch.cuda._sleep(0)
+    e1.record()
+    torch.cuda.synchronize()
+    return round(e0.elapsed_time(e1) * 1e3 / reps, 3)
 
 
 def copy_calibration(device, mb=512):
