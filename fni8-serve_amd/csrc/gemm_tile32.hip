@@ -127,49 +127,73 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
 
     // Fragment read: lane l takes row l%32 of a 32-row block and the k-half
     // (l/32)*16 of each 32-byte k sub-step -- the 32x32x32 operand layout.
+    // Only the wave's first LIVE 32-row blocks are computed: in a segment's last
+    // row tile the blocks wholly past its end are skipped (their accumulators stay
+    // zero and their rows are never written).
     const int fo = (lane & 31) * LDSR + (lane >> 5) * 16;
-    auto compute = [&](auto buf_c) {
+    auto compute = [&](auto buf_c, auto live_c) {
         constexpr int buf = decltype(buf_c)::value;
-        const int8_t* ab = smem + buf * BUF + (wm * WTM) * LDSR + fo;
-        const int8_t* bb = smem + buf * BUF + (BM + wn * WTN) * LDSR + fo;
+        constexpr int LIVE = decltype(live_c)::value;
+        if constexpr (LIVE > 0) {
+            const int8_t* ab = smem + buf * BUF + (wm * WTM) * LDSR + fo;
+            const int8_t* bb = smem + buf * BUF + (BM + wn * WTN) * LDSR + fo;
 #pragma unroll
-        for (int ks = 0; ks < BK / 32; ks++) {
-            i32x4 af[FM], bf[FN];
+            for (int ks = 0; ks < BK / 32; ks++) {
+                i32x4 af[LIVE], bf[FN];
 #pragma unroll
-            for (int i = 0; i < FM; i++)
-                af[i] = *reinterpret_cast<const i32x4*>(ab + i * 32 * LDSR + ks * 32);
-#pragma unroll
-            for (int j = 0; j < FN; j++)
-                bf[j] = *reinterpret_cast<const i32x4*>(bb + j * 32 * LDSR + ks * 32);
-#pragma unroll
-            for (int i = 0; i < FM; i++)
+                for (int i = 0; i < LIVE; i++)
+                    af[i] = *reinterpret_cast<const i32x4*>(ab + i * 32 * LDSR + ks * 32);
 #pragma unroll
                 for (int j = 0; j < FN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    bf[j] = *reinterpret_cast<const i32x4*>(bb + j * 32 * LDSR + ks * 32);
+#pragma unroll
+                for (int i = 0; i < LIVE; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] =
+                            __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+            }
         }
     };
 
     using C0 = std::integral_constant<int, 0>;
     using C1 = std::integral_constant<int, 1>;
     const int KT = K / BK;  // even and >= 2 (checked by the launcher)
-    gload(0, C0{});
-    gload(1, C1{});
-    sstore(C0{}, C0{});
-    lds_barrier();
-    for (int kt = 0; kt < KT - 2; kt += 2) {
-        gload(kt + 2, C0{});
-        compute(C0{});
-        sstore(C1{}, C1{});
-        lds_barrier();
-        gload(kt + 3, C1{});
-        compute(C1{});
+    // Every variant runs the same loads, LDS stores and barriers; only the
+    // MFMA work differs.
+    auto mainloop = [&](auto live_c) {
+        gload(0, C0{});
+        gload(1, C1{});
         sstore(C0{}, C0{});
         lds_barrier();
+        for (int kt = 0; kt < KT - 2; kt += 2) {
+            gload(kt + 2, C0{});
+            compute(C0{}, live_c);
+            sstore(C1{}, C1{});
+            lds_barrier();
+            gload(kt + 3, C1{});
+            compute(C1{}, live_c);
+            sstore(C0{}, C0{});
+            lds_barrier();
+        }
+        compute(C0{}, live_c);
+        sstore(C1{}, C1{});
+        lds_barrier();
+        compute(C1{}, live_c);
+    };
+    if constexpr (GROUPED && FM <= 2) {
+        // live 32-row blocks of this wave, made wave-uniform (scalar branch)
+        const int left = m1 - m0 - wm * WTM;
+        const int live = __builtin_amdgcn_readfirstlane(left <= 0 ? 0 : (left + 31) >> 5);
+        if (live >= FM)
+            mainloop(std::integral_constant<int, FM>{});
+        else if (live == 1)
+            mainloop(C1{});
+        else
+            mainloop(C0{});
+    } else {
+        mainloop(std::integral_constant<int, FM>{});
     }
-    compute(C0{});
-    sstore(C1{}, C1{});
-    lds_barrier();
-    compute(C1{});
     __syncthreads();  // every wave is done with the LDS stages
 
     tile_epilogue<BM, BN, GROUPED, WRITE_ACC>(acc, smem, tid, lane, wm, 0, wn * (BN / 4), m0, m1,
