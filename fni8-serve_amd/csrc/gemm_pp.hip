@@ -28,8 +28,10 @@
 // k-order inside a k-tile changes, identically for A and B, which leaves every
 // int32 dot product unchanged.
 //
-// Epilogue: the accumulators go through LDS as int32 (half the tile at a time)
-// and come back as coalesced rows; fp16(((float)acc * as[m]) * ws[n] (+ bias[n])).
+// The MFMAs compute D = W * X^T (weight fragment first), so each lane ends with
+// four consecutive output columns per register group; the epilogue
+// (tile_common.h) dequantizes in registers, stages the fp16 tile once in LDS and
+// writes coalesced 16-byte row chunks.
 #include <type_traits>
 
 #include "tile_common.h"
@@ -85,6 +87,10 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     int m0, m1, n0;
     fni8t::dense_tile<BM, BN>(M, N, m0, m1, n0);
     const int KT = K / BK;
+    // the epilogue's scales, issued before every copy: the waits for the first
+    // k-tile cover them
+    const fni8t::TileScales tsc =
+        fni8t::load_tile_scales<BM, BN, false>(tid, m0, m1, n0, N, nullptr, as, ws, bias);
 
     // Copy sources.  Instruction i of wave w fills stage slots [(w*D+i)*64, +64)
     // (16-byte slots; row = slot / 8); rows past the tile's end repeat its last
@@ -189,7 +195,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
                     for (int i = 0; i < FM; i++)
 #pragma unroll
                         for (int j = 0; j < FN; j++)
-                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(af[ks][i], bf[ks][j],
+                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[ks][j], af[ks][i],
                                                                               acc[i][j], 0, 0, 0);
                 __builtin_amdgcn_s_setprio(0);
                 if (g == 0 && h == 1 && t + 1 < KT) wait_vmcnt<0>();
@@ -198,11 +204,12 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
         }
     }
     if (g == 0) slot_barrier();
+    float* sl = reinterpret_cast<float*>(smem + fni8t::tile_scale_offset<BM, BN>(2 * STAGE));
+    fni8t::store_tile_scales<BM, BN>(tsc, sl, tid);
     __syncthreads();  // every copy has landed and every wave is done with the stages
 
-    fni8t::tile_epilogue<BM, BN, false, WRITE_ACC, FM, FN>(
-        acc, smem, tid, lane, g, wrow - g * (BM / 2), wcol, m0, m1, n0, N, nullptr, as, ws, bias,
-        y, ldy, acc_out);
+    fni8t::tile_epilogue<BM, BN, WRITE_ACC, FM, FN>(acc, smem, sl, tid, lane, wrow, wcol, m0, m1,
+                                                    n0, N, bias != nullptr, y, ldy, acc_out);
 }
 
 template <int BM, int BN, int WC = 4>
@@ -210,8 +217,8 @@ int launch(const int8_t* aq, int64_t lda, const float* as, int M, int K, const i
            const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
            int32_t* acc_out, hipStream_t st) {
     constexpr size_t main_lds = (size_t)2 * (BM + BN) * 128;
-    constexpr size_t epi_lds = fni8t::tile_epilogue_lds<BM, BN>();
-    constexpr size_t lds = main_lds > epi_lds ? main_lds : epi_lds;
+    constexpr size_t lds =
+        fni8t::tile_scale_offset<BM, BN>(main_lds) + fni8t::tile_scale_lds<BM, BN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
     const dim3 grid(((N + BN - 1) / BN) * (unsigned)((M + BM - 1) / BM));
     // The LDS limit is a per-function attribute: each instantiation sets it once

@@ -12,11 +12,10 @@
 // steady-state loop is branch-free (two steps per trip, tail peeled), which
 // keeps every register-array index static.
 //
-// Epilogue: the accumulators go to LDS as int32 (half the tile at a time),
-// then every thread streams 16-byte rows back, applies
-// fp16(((float)acc * as[m]) * ws[n] (+ bias[n])) with a wave-uniform row scale
-// and writes 8 contiguous bytes per lane -- coalesced output with almost no
-// live registers.
+// The MFMAs compute D = W * X^T (weight fragment first); the epilogue
+// (tile_common.h) dequantizes fp16(((float)acc * as[m]) * ws[n] (+ bias[n])) in
+// registers, stages the fp16 tile once in LDS and writes coalesced 16-byte row
+// chunks.
 #include <type_traits>
 
 #include "tile_common.h"
@@ -73,6 +72,10 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
     } else {
         dense_tile<BM, BN>(M, N, m0, m1, n0);
     }
+    // the epilogue's scales, issued before the operand loads (the main loop's
+    // waits cover them)
+    const fni8t::TileScales tsc = fni8t::load_tile_scales<BM, BN, GROUPED>(
+        tid, m0, m1, n0, N, row_index, as, wsexp, bexp);
 
     // Global sources of this thread's chunks; rows past the end are clamped to
     // the last valid row (their products land in rows that are never written).
@@ -151,7 +154,7 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
 #pragma unroll
                     for (int j = 0; j < FN; j++)
                         acc[i][j] =
-                            __builtin_amdgcn_mfma_i32_32x32x32_i8(af[i], bf[j], acc[i][j], 0, 0, 0);
+                            __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
             }
         }
     };
@@ -194,10 +197,12 @@ __global__ __launch_bounds__(512) void gemm_tile32_kernel(
     } else {
         mainloop(std::integral_constant<int, FM>{});
     }
+    float* sl = reinterpret_cast<float*>(smem + fni8t::tile_scale_offset<BM, BN>(2 * BUF));
+    fni8t::store_tile_scales<BM, BN>(tsc, sl, tid);
     __syncthreads();  // every wave is done with the LDS stages
 
-    tile_epilogue<BM, BN, GROUPED, WRITE_ACC>(acc, smem, tid, lane, wm, 0, wn * (BN / 4), m0, m1,
-                                              n0, N, row_index, as, wsexp, bexp, y, ldy, acc_out);
+    tile_epilogue<BM, BN, WRITE_ACC, FM, FN>(acc, smem, sl, tid, lane, wm * WTM, wn * WTN, m0, m1,
+                                             n0, N, bexp != nullptr, y, ldy, acc_out);
 }
 
 template <int BM, int BN, int BK, bool GROUPED>
@@ -206,8 +211,8 @@ int launch(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_in
            const uint16_t* bias, uint16_t* y, int64_t ldy, int32_t* acc_out, unsigned slots,
            hipStream_t st) {
     constexpr size_t main_lds = 2 * (BM + BN) * (BK + 16);
-    constexpr size_t epi_lds = fni8t::tile_epilogue_lds<BM, BN>();
-    constexpr size_t lds = main_lds > epi_lds ? main_lds : epi_lds;
+    constexpr size_t lds =
+        fni8t::tile_scale_offset<BM, BN>(main_lds) + fni8t::tile_scale_lds<BM, BN>();
     static_assert(lds <= 160 * 1024, "LDS budget");
     const unsigned ntn = (unsigned)((N + BN - 1) / BN);
     // grouped: an upper bound of the work items (slots row tiles per n-tile)

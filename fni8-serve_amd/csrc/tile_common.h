@@ -1,6 +1,6 @@
 // Tile helpers shared by the 8-wave MFMA GEMM kernels (gemm_tile32.hip,
 // gemm_pp.hip): the XCD-aware order of dense tiles and the LDS-staged fp16
-// epilogue of a 2 x 4 wave layout of 32x32 accumulator blocks.
+// epilogue of 32x32 accumulator blocks.
 #pragma once
 
 #include "common.h"
@@ -29,108 +29,165 @@ __device__ __forceinline__ void dense_tile(int M, int N, int& m0, int& m1, int& 
     n0 = (in_group / gsize) * BN;
 }
 
-// LDS bytes the epilogue needs: row scales, column scales, bias as fp32, and
-// half the tile as int32 (rows padded by 8 columns).
+// ---- epilogue ---------------------------------------------------------------
+// The kernels issue their MFMAs as D = W * X^T (weight fragment as the A
+// operand), so a 32x32 accumulator block of lane l holds token row l % 32 and,
+// in registers 4q..4q+3, the four consecutive output columns
+// 8q + 4*(l/32) + 0..3.  The epilogue dequantizes in registers,
+// fp16(((float)acc * as[m]) * ws[n] (+ bias[n])) with a per-lane row scale,
+// stages the fp16 tile in LDS once (8-byte writes), and streams it back as
+// 16-byte row chunks.
+//
+// LDS: the fp16 tile at offset 0 (it overlaps the main loop's stages, which
+// are dead by then), and the scales (row scales, column scales, bias as fp32)
+// in a region of their own at tile_scale_offset, written before the last
+// barrier of the main loop.
 template <int BM, int BN>
-constexpr size_t tile_epilogue_lds() {
-    return (size_t)(BM + 2 * BN) * 4 + (size_t)(BM / 2) * (BN + 8) * 4;
+constexpr size_t tile_stage_lds() {
+    return (size_t)BM * BN * 2;
+}
+template <int BM, int BN>
+constexpr size_t tile_scale_lds() {
+    return (size_t)(BM + 2 * BN) * 4;
+}
+// Offset of the scale region given the main loop's LDS bytes; the kernel's LDS
+// is tile_scale_offset + tile_scale_lds.
+template <int BM, int BN>
+constexpr size_t tile_scale_offset(size_t main_lds) {
+    return main_lds > tile_stage_lds<BM, BN>() ? main_lds : tile_stage_lds<BM, BN>();
 }
 
-// Epilogue of the tile kernels (8 waves, 2 x 4): the accumulators go to LDS as
-// int32 (half the tile at a time), then every thread streams 16-byte rows back,
-// applies fp16(((float)acc * as[m]) * ws[n] (+ bias[n])) with a wave-uniform row
-// scale and writes 8 contiguous bytes per lane.  Column scales and the bias
-// (converted to fp32 once, which is exact) are staged in LDS and read four at a
-// time.  The caller has finished with its LDS stages (a barrier before the call).
-// wm: the wave's half of the tile (rows wm*BM/2..); roff, coff: the row (inside
-// that half) and column of the wave's first 32x32 block.
-template <int BM, int BN, bool GROUPED, bool WRITE_ACC, int FM = BM / 64, int FN = BN / 128>
-__device__ __forceinline__ void tile_epilogue(const i32x16 (&acc)[FM][FN], int8_t* smem, int tid,
-                                              int lane, int wm, int roff, int coff, int m0, int m1, int n0,
-                                              int N, const int32_t* __restrict__ row_index,
-                                              const float* __restrict__ as,
-                                              const float* __restrict__ wsexp,
-                                              const uint16_t* __restrict__ bexp,
-                                              uint16_t* __restrict__ y, int64_t ldy,
-                                              int32_t* __restrict__ acc_out) {
-    constexpr int NT = 512;
-    constexpr int HALF = BM / 2;          // rows staged per pass (one wave-row)
-    constexpr int OTS = BN + 8;           // int32 row stride of the staging tile
-    float* as_l = reinterpret_cast<float*>(smem);
-    float* ws_l = as_l + BM;
-    float* b_l = ws_l + BN;
-    int32_t* ot = reinterpret_cast<int32_t*>(b_l + BN);
-    const bool has_bias = bexp != nullptr;
-    for (int t = tid; t < BM; t += NT) {
-        const int mr = m0 + t;
-        float v = 0.f;
-        if (mr < m1) v = as[(GROUPED && row_index != nullptr) ? row_index[mr] : mr];
-        as_l[t] = v;
+// Thread t's share of the scales (row scale of tile row t for t < BM, column
+// scale and bias of tile column t for t < BN; 0 past the tile's edge), loaded
+// at kernel start so that their latency hides behind the main loop.  Nothing
+// uses them before store_tile_scales (the bias stays raw fp16 bits until then,
+// and its conversion to fp32 is exact), so no wait is placed on them early.
+struct TileScales {
+    float a, w;
+    uint32_t b;
+};
+template <int BM, int BN, bool GROUPED>
+__device__ __forceinline__ TileScales load_tile_scales(int tid, int m0, int m1, int n0, int N,
+                                                       const int32_t* __restrict__ row_index,
+                                                       const float* __restrict__ as,
+                                                       const float* __restrict__ wsexp,
+                                                       const uint16_t* __restrict__ bexp) {
+    TileScales v{0.f, 0.f, 0u};
+    if (tid < BM && m0 + tid < m1) {
+        const int mr = m0 + tid;
+        v.a = as[(GROUPED && row_index != nullptr) ? row_index[mr] : mr];
     }
-    for (int t = tid; t < BN; t += NT) {
-        const bool in = n0 + t < N;
-        ws_l[t] = in ? wsexp[n0 + t] : 0.f;
-        b_l[t] = (in && has_bias) ? fni8::h2f(bexp[n0 + t]) : 0.f;
+    if (tid < BN && n0 + tid < N) {
+        v.w = wsexp[n0 + tid];
+        if (bexp != nullptr) v.b = bexp[n0 + tid];
     }
+    return v;
+}
+template <int BM, int BN>
+__device__ __forceinline__ void store_tile_scales(const TileScales& v, float* sl, int tid) {
+    if (tid < BM) sl[tid] = v.a;
+    if (tid < BN) {
+        sl[BM + tid] = v.w;
+        // converted here, in an instruction the compiler cannot hoist next to
+        // the load (which would put a wait for it in front of the main loop)
+        float bf;
+        asm volatile("v_cvt_f32_f16 %0, %1" : "=v"(bf) : "v"(v.b));
+        sl[BM + BN + tid] = bf;
+    }
+}
 
+// two fp32 -> packed fp16, round to nearest even (the rounding of v_cvt_f16_f32)
+__device__ __forceinline__ uint32_t cvt_pk_f16(float lo, float hi) {
+    uint32_t r;
+    asm("v_cvt_pk_f16_f32 %0, %1, %2" : "=v"(r) : "v"(lo), "v"(hi));
+    return r;
+}
+
+// 8-byte unit u of staged row r sits at unit u ^ (r & 15): the 16 rows of one
+// write pass (lanes 16k..16k+15) land in 16 distinct units of 128 bytes.
+// Needs BN % 64 == 0 (whole 16-unit groups per row).
+//
+// Preconditions: the caller's accumulators are complete, store_tile_scales has
+// run, and a workgroup barrier followed both (the main loop's LDS is dead).
+// roff, coff: tile-local row and column of the wave's first 32x32 block.
+template <int BM, int BN, bool WRITE_ACC, int FM, int FN>
+__device__ __forceinline__ void tile_epilogue(const i32x16 (&acc)[FM][FN], int8_t* smem,
+                                              const float* sl, int tid, int lane, int roff,
+                                              int coff, int m0, int m1, int n0, int N,
+                                              bool has_bias, uint16_t* __restrict__ y,
+                                              int64_t ldy, int32_t* __restrict__ acc_out) {
+    static_assert(BN % 64 == 0, "staging swizzle works on 128-byte groups");
+    constexpr int NT = 512;
+    constexpr int RS = BN * 2;  // bytes per staged row
+    const float* as_l = sl;
+    const float* ws_l = sl + BM;
+    const float* b_l = sl + BM + BN;
+    uint8_t* st = reinterpret_cast<uint8_t*>(smem);
+    const int lr = lane & 31, lh = lane >> 5;
 #pragma unroll
-    for (int pass = 0; pass < 2; pass++) {
-        if (wm == pass) {
-            // lane l, register r of block (i, j): row 8*(r/4) + 4*(l/32) + r%4, col l%32
+    for (int i = 0; i < FM; i++) {
+        const int row = roff + i * 32 + lr;
+        const float asc = as_l[row];
+        const int sw = row & 15;
 #pragma unroll
-            for (int i = 0; i < FM; i++)
+        for (int j = 0; j < FN; j++)
 #pragma unroll
-                for (int j = 0; j < FN; j++)
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const int row = roff + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                        const int col = coff + j * 32 + (lane & 31);
-                        ot[row * OTS + col] = acc[i][j][r];
-                    }
-        }
-        __syncthreads();
-        // stream the staged half: BN/4 chunks of 4 columns per row; a wave covers
-        // whole rows, so the row scale is uniform across the wave
-        constexpr int CHR = BN / 4;
-        for (int c = tid; c < HALF * CHR; c += NT) {
-            const int rl = c / CHR, cl = (c % CHR) * 4;
-            const int row_t = pass * HALF + rl;
-            const int mr = m0 + row_t;
-            const int col = n0 + cl;
-            if (mr >= m1 || col >= N) continue;
-            const i32x4 a4 = *reinterpret_cast<const i32x4*>(ot + rl * OTS + cl);
-            const float4 w4 = *reinterpret_cast<const float4*>(ws_l + cl);
-            const float asc = as_l[row_t];
-            float v[4] = {(float)a4[0] * asc, (float)a4[1] * asc, (float)a4[2] * asc,
-                          (float)a4[3] * asc};
-            v[0] = v[0] * w4.x;
-            v[1] = v[1] * w4.y;
-            v[2] = v[2] * w4.z;
-            v[3] = v[3] * w4.w;
-            if (has_bias) {
-                const float4 b4 = *reinterpret_cast<const float4*>(b_l + cl);
-                v[0] = v[0] + b4.x;
-                v[1] = v[1] + b4.y;
-                v[2] = v[2] + b4.z;
-                v[3] = v[3] + b4.w;
-            }
-            uint16_t h[4];
-#pragma unroll
-            for (int q = 0; q < 4; q++) h[q] = fni8::f2h(v[q]);
-            uint16_t* yp = y + (int64_t)mr * ldy + col;
-            if (col + 3 < N && ((uintptr_t)yp & 7) == 0) {
+            for (int q = 0; q < 4; q++) {
+                const int col = coff + j * 32 + 8 * q + 4 * lh;
+                const float4 w4 = *reinterpret_cast<const float4*>(ws_l + col);
+                float v0 = (float)acc[i][j][4 * q + 0] * asc;
+                float v1 = (float)acc[i][j][4 * q + 1] * asc;
+                float v2 = (float)acc[i][j][4 * q + 2] * asc;
+                float v3 = (float)acc[i][j][4 * q + 3] * asc;
+                v0 = v0 * w4.x;
+                v1 = v1 * w4.y;
+                v2 = v2 * w4.z;
+                v3 = v3 * w4.w;
+                if (has_bias) {
+                    const float4 b4 = *reinterpret_cast<const float4*>(b_l + col);
+                    v0 = v0 + b4.x;
+                    v1 = v1 + b4.y;
+                    v2 = v2 + b4.z;
+                    v3 = v3 + b4.w;
+                }
                 uint2 pk;
-                pk.x = h[0] | ((uint32_t)h[1] << 16);
-                pk.y = h[2] | ((uint32_t)h[3] << 16);
-                *reinterpret_cast<uint2*>(yp) = pk;
-            } else {
-                for (int q = 0; q < 4 && col + q < N; q++) yp[q] = h[q];
+                pk.x = cvt_pk_f16(v0, v1);
+                pk.y = cvt_pk_f16(v2, v3);
+                *reinterpret_cast<uint2*>(st + row * RS + (((col >> 2) ^ sw) << 3)) = pk;
+                if constexpr (WRITE_ACC) {
+                    const int mr = m0 + row, n = n0 + col;
+                    if (mr < m1) {
+                        int32_t* ap = acc_out + (int64_t)mr * N + n;
+#pragma unroll
+                        for (int t = 0; t < 4; t++)
+                            if (n + t < N) ap[t] = acc[i][j][4 * q + t];
+                    }
+                }
             }
-            if constexpr (WRITE_ACC) {
-                for (int q = 0; q < 4 && col + q < N; q++) acc_out[(int64_t)mr * N + col + q] = a4[q];
-            }
+    }
+    __syncthreads();
+    constexpr int CPR = BN / 8;  // 16-byte chunks per row
+    for (int c = tid; c < BM * CPR; c += NT) {
+        const int row = c / CPR, k = c % CPR;
+        const int mr = m0 + row, col = n0 + k * 8;
+        if (mr >= m1 || col >= N) continue;
+        const int sw = row & 15;
+        uint4 v = *reinterpret_cast<const uint4*>(st + row * RS + (((2 * k) ^ (sw & 14)) << 3));
+        if (sw & 1) {  // the two 8-byte units came back swapped
+            const uint32_t x0 = v.x, x1 = v.y;
+            v.x = v.z;
+            v.y = v.w;
+            v.z = x0;
+            v.w = x1;
         }
-        __syncthreads();
+        uint16_t* yp = y + (int64_t)mr * ldy + col;
+        if (col + 7 < N && ((uintptr_t)yp & 15) == 0) {
+            *reinterpret_cast<uint4*>(yp) = v;
+        } else {
+            const uint32_t w32[4] = {v.x, v.y, v.z, v.w};
+            for (int t = 0; t < 8 && col + t < N; t++)
+                yp[t] = (uint16_t)(w32[t >> 1] >> (16 * (t & 1)));
+        }
     }
 }
 
