@@ -3,6 +3,8 @@
 // epilogue of 32x32 accumulator blocks.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace fni8t {
@@ -124,69 +126,117 @@ __device__ __forceinline__ void tile_epilogue(const i32x16 (&acc)[FM][FN], int8_
     const float* b_l = sl + BM + BN;
     uint8_t* st = reinterpret_cast<uint8_t*>(smem);
     const int lr = lane & 31, lh = lane >> 5;
+    // roff is a multiple of 32, so the lane's staged rows all share the swizzle
+    // lr & 15, and its write offsets depend on (j, q) only
+    const int sw = lr & 15;
+    uint8_t* wbase = st + (roff + lr) * RS;
+    int woff[FN][4];
 #pragma unroll
-    for (int i = 0; i < FM; i++) {
-        const int row = roff + i * 32 + lr;
-        const float asc = as_l[row];
-        const int sw = row & 15;
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            woff[j][q] = ((((coff + j * 32 + 8 * q + 4 * lh) >> 2) ^ sw) << 3);
+    auto convert = [&](auto bias_c) {
+        constexpr bool BIAS = decltype(bias_c)::value;
+        // column scales (and bias) of the lane's 4*FN*4 columns, read once
+        float4 w4[FN][4], b4[FN][4];
 #pragma unroll
         for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int col = coff + j * 32 + 8 * q + 4 * lh;
-                const float4 w4 = *reinterpret_cast<const float4*>(ws_l + col);
-                float v0 = (float)acc[i][j][4 * q + 0] * asc;
-                float v1 = (float)acc[i][j][4 * q + 1] * asc;
-                float v2 = (float)acc[i][j][4 * q + 2] * asc;
-                float v3 = (float)acc[i][j][4 * q + 3] * asc;
-                v0 = v0 * w4.x;
-                v1 = v1 * w4.y;
-                v2 = v2 * w4.z;
-                v3 = v3 * w4.w;
-                if (has_bias) {
-                    const float4 b4 = *reinterpret_cast<const float4*>(b_l + col);
-                    v0 = v0 + b4.x;
-                    v1 = v1 + b4.y;
-                    v2 = v2 + b4.z;
-                    v3 = v3 + b4.w;
-                }
-                uint2 pk;
-                pk.x = cvt_pk_f16(v0, v1);
-                pk.y = cvt_pk_f16(v2, v3);
-                *reinterpret_cast<uint2*>(st + row * RS + (((col >> 2) ^ sw) << 3)) = pk;
-                if constexpr (WRITE_ACC) {
-                    const int mr = m0 + row, n = n0 + col;
-                    if (mr < m1) {
-                        int32_t* ap = acc_out + (int64_t)mr * N + n;
+                w4[j][q] = *reinterpret_cast<const float4*>(ws_l + col);
+                if constexpr (BIAS) b4[j][q] = *reinterpret_cast<const float4*>(b_l + col);
+            }
 #pragma unroll
-                        for (int t = 0; t < 4; t++)
-                            if (n + t < N) ap[t] = acc[i][j][4 * q + t];
+        for (int i = 0; i < FM; i++) {
+            const int row = roff + i * 32 + lr;
+            const float asc = as_l[row];
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float v0 = (float)acc[i][j][4 * q + 0] * asc;
+                    float v1 = (float)acc[i][j][4 * q + 1] * asc;
+                    float v2 = (float)acc[i][j][4 * q + 2] * asc;
+                    float v3 = (float)acc[i][j][4 * q + 3] * asc;
+                    v0 = v0 * w4[j][q].x;
+                    v1 = v1 * w4[j][q].y;
+                    v2 = v2 * w4[j][q].z;
+                    v3 = v3 * w4[j][q].w;
+                    if constexpr (BIAS) {
+                        v0 = v0 + b4[j][q].x;
+                        v1 = v1 + b4[j][q].y;
+                        v2 = v2 + b4[j][q].z;
+                        v3 = v3 + b4[j][q].w;
+                    }
+                    uint2 pk;
+                    pk.x = cvt_pk_f16(v0, v1);
+                    pk.y = cvt_pk_f16(v2, v3);
+                    *reinterpret_cast<uint2*>(wbase + i * 32 * RS + woff[j][q]) = pk;
+                    if constexpr (WRITE_ACC) {
+                        const int mr = m0 + row, n = n0 + coff + j * 32 + 8 * q + 4 * lh;
+                        if (mr < m1) {
+                            int32_t* ap = acc_out + (int64_t)mr * N + n;
+#pragma unroll
+                            for (int t = 0; t < 4; t++)
+                                if (n + t < N) ap[t] = acc[i][j][4 * q + t];
+                        }
                     }
                 }
-            }
-    }
+        }
+    };
+    if (has_bias)
+        convert(std::true_type{});
+    else
+        convert(std::false_type{});
     __syncthreads();
+
     constexpr int CPR = BN / 8;  // 16-byte chunks per row
-    for (int c = tid; c < BM * CPR; c += NT) {
-        const int row = c / CPR, k = c % CPR;
-        const int mr = m0 + row, col = n0 + k * 8;
-        if (mr >= m1 || col >= N) continue;
-        const int sw = row & 15;
-        uint4 v = *reinterpret_cast<const uint4*>(st + row * RS + (((2 * k) ^ (sw & 14)) << 3));
-        if (sw & 1) {  // the two 8-byte units came back swapped
+    // one 16-byte chunk back from LDS in logical order (the two 8-byte units of
+    // an odd-swizzled row come back swapped)
+    auto fetch = [&](int row, int k) {
+        const int rsw = row & 15;
+        uint4 v = *reinterpret_cast<const uint4*>(st + row * RS + (((2 * k) ^ (rsw & 14)) << 3));
+        if (rsw & 1) {
             const uint32_t x0 = v.x, x1 = v.y;
             v.x = v.z;
             v.y = v.w;
             v.z = x0;
             v.w = x1;
         }
-        uint16_t* yp = y + (int64_t)mr * ldy + col;
+        return v;
+    };
+    auto put = [&](uint16_t* yp, int col, uint4 v) {
         if (col + 7 < N && ((uintptr_t)yp & 15) == 0) {
             *reinterpret_cast<uint4*>(yp) = v;
         } else {
             const uint32_t w32[4] = {v.x, v.y, v.z, v.w};
             for (int t = 0; t < 8 && col + t < N; t++)
                 yp[t] = (uint16_t)(w32[t >> 1] >> (16 * (t & 1)));
+        }
+    };
+    if constexpr (NT % CPR == 0 && (NT / CPR) % 16 == 0) {
+        // each thread keeps one column chunk and steps by NT/CPR rows (a
+        // multiple of 16, so its swizzle is fixed)
+        constexpr int RSTEP = NT / CPR;
+        const int k = tid % CPR, r0 = tid / CPR;
+        const int col = n0 + k * 8;
+        if (col < N) {
+            uint16_t* yp = y + (int64_t)(m0 + r0) * ldy + col;
+#pragma unroll
+            for (int it = 0; it < BM / RSTEP; it++) {
+                const int row = r0 + it * RSTEP;
+                if (m0 + row < m1) put(yp, col, fetch(row, k));
+                yp += (int64_t)RSTEP * ldy;
+            }
+        }
+    } else {
+        for (int c = tid; c < BM * CPR; c += NT) {
+            const int row = c / CPR, k = c % CPR;
+            const int mr = m0 + row, col = n0 + k * 8;
+            if (mr >= m1 || col >= N) continue;
+            put(y + (int64_t)mr * ldy + col, col, fetch(row, k));
         }
     }
 }

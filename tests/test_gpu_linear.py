@@ -166,6 +166,54 @@ def test_prefill_bias_shipped_kernel(pkg, wl, cuda):
 
 
 @pytest.mark.parametrize("want_acc", [False, True])
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 1024), (600, 1003, 512)])
+def test_tile_epilogue_special_values(pkg, cuda, M, N, K, want_acc):
+    """The tile kernels' epilogue (the ping-pong kernel at 4096x4096, the 8-wave
+    tile kernel at 600x1003: ragged columns, rows not 16-byte aligned) on scales chosen to push fp16 outputs to overflow
+    (inf), into the subnormal range, to signed zeros (all-zero rows, zero and
+    -0 column scales and bias) and to NaN (one NaN row scale): fp16 bits against
+    the oracle's epilogue on sampled rows, NaN positions against NaN positions."""
+    rng = np.random.default_rng(7000 + M)
+    xq = rng.integers(-127, 128, size=(M, K), dtype=np.int8)
+    xq[3] = 0
+    xq[M - 2] = 0
+    q = rng.integers(-127, 128, size=(N, K), dtype=np.int8)
+    xs = (10.0 ** rng.uniform(-12, 2, size=M)).astype(np.float32)
+    xs[rng.random(M) < 0.25] *= -1
+    xs[3] = 1.0                # zero row: +0 * s, and -0 where s < 0 and bias is -0
+    xs[5] = np.float32(1e3)    # |acc| ~1e5 -> overflow
+    xs[6] = np.float32(1e-10)  # products in the fp16 subnormal range
+    xs[7] = np.nan
+    s = (10.0 ** rng.uniform(-6, 0, size=N)).astype(np.float32)
+    s[rng.random(N) < 0.3] *= -1
+    s[1] = 0.0
+    s[2] = -0.0
+    s[4] = np.float32(-1e-3)
+    bias = (rng.standard_normal(N) * 1e-3).astype(np.float16)
+    bias[rng.random(N) < 0.5] = 0
+    bias[4] = np.float16(-0.0)
+    qt = pkg.QTensor(torch.from_numpy(q).cuda(), torch.from_numpy(s).cuda(), scheme="per_row_i8")
+    out = pkg.gemm_w8a8(torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda(), qt,
+                            torch.from_numpy(bias).cuda(), want_acc=want_acc)
+    torch.cuda.synchronize()
+    y, acc = out if want_acc else (out, None)
+    rows = np.unique(np.concatenate([np.arange(0, 9), _sample_rows(M, M + N), [M - 2, M - 1]]))
+    accr = oracle.gemm_i8(xq[rows], q)
+    if want_acc:
+        assert np.array_equal(acc.cpu().numpy()[rows], accr), "int32 accumulators differ"
+    yr = oracle.dequant_f16(accr, xs[rows], s, bias).view(np.uint16)
+    yb = _f16bits(y)[rows]
+    nan_r = np.isnan(yr.view(np.float16))
+    assert np.array_equal(np.isnan(yb.view(np.float16)), nan_r), "NaN positions differ"
+    assert np.array_equal(yb[~nan_r], yr[~nan_r]), "fp16 outputs differ"
+    yf = yr.view(np.float16)
+    # the chosen scales really reach every special class
+    assert np.isinf(yf).any() and nan_r.any()
+    assert ((yf != 0) & (np.abs(yf.astype(np.float32)) < 2.0 ** -14)).any()
+    assert (yr == 0x8000).any() and (yr == 0).any()
+
+
+@pytest.mark.parametrize("want_acc", [False, True])
 def test_prefill_tile_192_ragged(pkg, wl, cuda, want_acc):
     """The 256x192 prefill tile (chosen when it fills the CUs in fewer
     tile-rounds) with a partial last row tile (2000 = 7*256 + 208) and a
