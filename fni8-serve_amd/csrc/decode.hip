@@ -33,6 +33,12 @@
 
 namespace {
 
+// Barrier that waits for LDS traffic only (the compiler's __syncthreads also
+// drains the weight loads in flight).
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ i32x4 ld16_nt(const int8_t* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
 }
@@ -42,7 +48,10 @@ __device__ __forceinline__ i32x4 ld16_nt(const int8_t* p) {
 // KCH: 16-byte chunks of each activation row per thread (K <= 16 * KCH * 64 *
 // WAVES / (FUSED ? 2 : 1)); FUSED: x is fp16 (quantized here), else x is int8
 // with scales xs_in.
-template <int MM, int RH, int WAVES, int SB, int KCH, bool FUSED>
+// EB: the prologue's barriers wait for LDS traffic only, and the second weight
+// batch is issued before the quantization (its latency then overlaps the
+// quantization's VALU work).
+template <int MM, int RH, int WAVES, int SB, int KCH, bool FUSED, bool EB = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
     const void* __restrict__ xin, int64_t ldx, const float* __restrict__ xs_in, int M, int K,
     const int8_t* __restrict__ w, const float* __restrict__ ws, int N,
@@ -113,7 +122,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
             am = fni8::wave_max_uniform(fni8::amax_fold(am));
             if (lane == 0) amx[wave * MM + m] = am;
         }
-        __syncthreads();
+        if constexpr (EB) {
+            lds_barrier();
+            if (nb > 1) load(wb, 1);
+        } else {
+            __syncthreads();
+        }
 #pragma unroll
         for (int m = 0; m < MM; m++) {
             uint32_t a = amx[m];
@@ -160,8 +174,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
             }
             if (tid == 0) scl[m] = m < M ? xs_in[m] : 0.f;
         }
+        if (EB && nb > 1) load(wb, 1);
     }
-    __syncthreads();
+    if constexpr (EB)
+        lds_barrier();
+    else
+        __syncthreads();
 
     // ---- weight stream ------------------------------------------------------
     int32_t acc[RH][MM];
@@ -194,7 +212,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
     };
     // steady state: prefetch batch b+1, consume batch b; the last batch is peeled
     for (int b = 0; b < nb - 1; b++) {
-        load(wb, b + 1);
+        if (!EB || b > 0) load(wb, b + 1);  // with EB, batch 1 went out in the prologue
         compute(wa, b);
 #pragma unroll
         for (int j = 0; j < SB; j++)
@@ -222,7 +240,7 @@ __global__ __launch_bounds__(WAVES * 64) void decode_gemv_kernel(
     }
 }
 
-template <int MM, int RH, int WAVES, int SB, int KCH, bool FUSED>
+template <int MM, int RH, int WAVES, int SB, int KCH, bool FUSED, bool EB = false>
 int launch_gemv(const void* x, int64_t ldx, const float* xs_in, int M, int K, const int8_t* w,
                 const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
                 int8_t* xq_out, float* xs_out, int32_t* acc_out, hipStream_t st) {
@@ -233,7 +251,7 @@ int launch_gemv(const void* x, int64_t ldx, const float* xs_in, int M, int K, co
     if ((int64_t)K > per_thread) return 1;
     const size_t lds = (size_t)MM * K + (size_t)WAVES * MM * ROWS * 4 + MM * 4 + WAVES * MM * 4;
     if (lds > 160 * 1024) return 1;
-    auto kern = decode_gemv_kernel<MM, RH, WAVES, SB, KCH, FUSED>;
+    auto kern = decode_gemv_kernel<MM, RH, WAVES, SB, KCH, FUSED, EB>;
     if (lds > 64 * 1024) {
         // The dynamic LDS limit is a per-function attribute; setting it again
         // with the same value is idempotent, so a race between threads is harmless.
@@ -265,12 +283,13 @@ int launch_decode_gemv(const void* x, int64_t ldx, const float* xs_in, int M, in
                        const int8_t* w, const float* ws, int N, const uint16_t* bias, uint16_t* y,
                        int64_t ldy, int8_t* xq_out, float* xs_out, int32_t* acc_out,
                        hipStream_t st) {
-#define FNI8_GEMV(MM, RH, WV, SB, KCH)                                                         \
+#define FNI8_GEMV_E(MM, RH, WV, SB, KCH, EB)                                                   \
     do {                                                                                       \
-        const int rc = launch_gemv<MM, RH, WV, SB, KCH, FUSED>(                                \
+        const int rc = launch_gemv<MM, RH, WV, SB, KCH, FUSED, EB>(                            \
             x, ldx, xs_in, M, K, w, ws, N, bias, y, ldy, xq_out, xs_out, acc_out, st);         \
         if (rc != 1) return rc;                                                                \
     } while (0)
+#define FNI8_GEMV(MM, RH, WV, SB, KCH) FNI8_GEMV_E(MM, RH, WV, SB, KCH, false)
 #define FNI8_GEMV_GENERIC(MM)                \
     do {                                     \
         if (K <= 4096) {                     \
@@ -304,7 +323,9 @@ int launch_decode_gemv(const void* x, int64_t ldx, const float* xs_in, int M, in
             else if (N <= 8192) FNI8_GEMV(2, 2, 4, 4, 2);
             else FNI8_GEMV(2, 4, 4, 4, 2);
         } else {
-            FNI8_GEMV(2, 2, 4, 4, 6);
+            // early second batch: down at 2 tokens 11.61 -> 10.73 us (QKV and
+            // gate_up lose 3-6% with it; O has a single batch per wave)
+            FNI8_GEMV_E(2, 2, 4, 4, 6, true);
         }
         FNI8_GEMV_GENERIC(2);
     }
@@ -317,6 +338,7 @@ int launch_decode_gemv(const void* x, int64_t ldx, const float* xs_in, int M, in
     FNI8_GEMV_GENERIC(4);
 #undef FNI8_GEMV_GENERIC
 #undef FNI8_GEMV
+#undef FNI8_GEMV_E
 }
 
 }  // namespace

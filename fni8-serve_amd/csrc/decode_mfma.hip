@@ -268,7 +268,9 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
 // The lane's fp16 chunks stay in registers between the max and the quantize
 // pass when there are at most 16 of them (MM * PQ <= 16); otherwise the
 // quantize pass loads them again (from cache: the max pass just read them).
-template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, int MM = 4>
+// EB: the second weight batch is issued after the row-max barrier, before the
+// quantization, so its latency overlaps the quantization's VALU work.
+template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, int MM = 4, bool EB = false>
 __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int M, int K, const int8_t* __restrict__ w,
     const float* __restrict__ ws, int N, const uint16_t* __restrict__ bias,
@@ -328,6 +330,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
         if (lane == 0) amx[wave * MM + m] = mx;
     }
     lds_barrier();
+    if constexpr (EB && NBT > 1) {
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < RB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)(SB + j) * 128);
+    }
     // 4. quantize this wave's share into its LDS area: token rows of 128 bytes per
     //    slab, 16-byte chunks swizzled by token (conflict-free A-operand reads)
     int8_t* xw = xarea + wave * XAREA;
@@ -395,10 +403,12 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     };
 #pragma unroll
     for (int bt = 0; bt < NBT - 1; bt++) {
+        if (!EB || bt > 0) {
 #pragma unroll
-        for (int j = 0; j < SB; j++)
+            for (int j = 0; j < SB; j++)
 #pragma unroll
-            for (int h = 0; h < RB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)((bt + 1) * SB + j) * 128);
+                for (int h = 0; h < RB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)((bt + 1) * SB + j) * 128);
+        }
         compute(wa, bt);
 #pragma unroll
         for (int j = 0; j < SB; j++)
@@ -439,7 +449,7 @@ int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const i
     return FNI8_OK;
 }
 
-template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, int MM = 4>
+template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, int MM = 4, bool EB = false>
 int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, const float* ws,
                  int N, const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
                  float* xs_out, int32_t* acc_out, hipStream_t st) {
@@ -453,7 +463,7 @@ int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, 
     if constexpr (lds > 160 * 1024) {
         return 1;
     } else {
-        auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ, RB, MM>;
+        auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ, RB, MM, EB>;
         static const bool ok = hipFuncSetAttribute((const void*)kern,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    160 * 1024) == hipSuccess;
@@ -551,20 +561,24 @@ int launch_grouped_mt(const int8_t* xq, int64_t ldx, const float* xs, const int3
 int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w,
                        const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
                        int8_t* xq_out, float* xs_out, int32_t* acc_out, hipStream_t st) {
-#define FNI8_DF_RB(NB, WV, SB, PQ, RB)                                                          \
+#define FNI8_DF_RBE(NB, WV, SB, PQ, RB, EB)                                                     \
     do {                                                                                        \
-        const int rc = launch_fused<NB, WV, SB, PQ, RB>(x, ldx, M, K, w, ws, N, bias, y, ldy,   \
-                                                        xq_out, xs_out, acc_out, st);           \
+        const int rc = launch_fused<NB, WV, SB, PQ, RB, 4, EB>(x, ldx, M, K, w, ws, N, bias, y, \
+                                                               ldy, xq_out, xs_out, acc_out, st); \
         if (rc != 1) return rc;                                                                 \
     } while (0)
+#define FNI8_DF_RB(NB, WV, SB, PQ, RB) FNI8_DF_RBE(NB, WV, SB, PQ, RB, false)
 #define FNI8_DF(NB, WV, SB, PQ) FNI8_DF_RB(NB, WV, SB, PQ, 2 * NB)
     const bool wide = N >= 16384, narrow = N <= 4096;
     if (wide) {
         FNI8_DF(2, 4, 2, 2);
         FNI8_DF(2, 8, 1, 3);
     } else if (narrow) {
-        FNI8_DF(1, 4, 4, 2);
-        FNI8_DF(1, 8, 3, 3);
+        // second weight batch issued before the quantization (O and down at 3-4
+        // tokens: 6.81 -> 6.23 and 12.88 -> 11.82 us; even or slower on QKV and
+        // gate_up, which keep the later issue)
+        FNI8_DF_RBE(1, 4, 4, 2, 2, true);
+        FNI8_DF_RBE(1, 8, 3, 3, 2, true);
     } else {
         if (prefer_24_rows(N)) FNI8_DF_RB(2, 8, 2, 1, 3);  // QKV: 24-row workgroups
         FNI8_DF(2, 8, 1, 1);
@@ -581,6 +595,7 @@ int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_
     FNI8_DF(1, 8, 1, 3);
 #undef FNI8_DF
 #undef FNI8_DF_RB
+#undef FNI8_DF_RBE
     return 1;
 }
 
