@@ -491,10 +491,11 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_mfma_kernel(
         for (int j = 0; j < SB; j++)
 #pragma unroll
             for (int h = 0; h < 2 * MT; h++)
+                if (h * 8 < M)  // load groups wholly past the last token are skipped
 #pragma unroll
-                for (int p = 0; p < 2; p++)
-                    dx[j][2 * h + p] =
-                        *reinterpret_cast<const i32x4*>(xsrc[h] + (s + j) * 256 + p * 128);
+                    for (int p = 0; p < 2; p++)
+                        dx[j][2 * h + p] =
+                            *reinterpret_cast<const i32x4*>(xsrc[h] + (s + j) * 256 + p * 128);
     };
 
     int8_t* st = smem + wave * (SB * TILE);
@@ -509,9 +510,10 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_mfma_kernel(
             for (int h = 0; h < 2 * NB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + woff[h]) = wv[j][h];
 #pragma unroll
             for (int h = 0; h < 2 * MT; h++)
+                if (h * 8 < M)  // rows past the last token keep stale values (never stored)
 #pragma unroll
-                for (int p = 0; p < 2; p++)
-                    *reinterpret_cast<i32x4*>(st + j * TILE + xoff[h][p]) = xv[j][2 * h + p];
+                    for (int p = 0; p < 2; p++)
+                        *reinterpret_cast<i32x4*>(st + j * TILE + xoff[h][p]) = xv[j][2 * h + p];
         }
         __builtin_amdgcn_wave_barrier();
         asm volatile("" ::: "memory");
