@@ -17,7 +17,7 @@
 // product does not care in which order its terms come.  Sign extension of a
 // nibble u in each byte is ((u ^ 8) + 0x78) ^ 0x80: the sum stays below 0x88,
 // so no carry crosses a byte.
-#include "common.h"
+#include "w4a8_common.h"
 
 namespace {
 
@@ -182,13 +182,6 @@ __global__ __launch_bounds__(kGemvThreads) void w4a8_gemv_kernel(
 // FUSED: x arrives as fp16 and is quantized here (the per-token quantization
 // of fni8_quantize_rowwise_f16, division-free, same bits); workgroup 0 also
 // writes xq and xs for the caller.
-// Waits for this wave's LDS traffic, then meets the other waves.  Unlike
-// __syncthreads it leaves the outstanding global loads (the next round's
-// weights) in flight.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // EB: the prologue's barriers wait for LDS traffic only, and the second weight
 // batch is issued before the quantization, so its latency overlaps that VALU work.
 template <int MM, int RH, int WAVES, int SB, int KCH, int CPG, bool FUSED, bool EB = false>
@@ -394,21 +387,7 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_stream_kernel(
 // elements through the round's groups in order.  The group-sum area is double
 // buffered, so one barrier per round suffices: a wave writes round r+2's sums
 // only after the barrier of round r+1, and every thread reaches that barrier
-// after folding round r.
-__device__ __forceinline__ int swz(int row, int chunk) {
-    return ((chunk ^ (row & 7) ^ ((row >> 3) & 7)) & 7) * 16;
-}
-
-// 8 packed bytes (16 codes) -> 16 int8 in natural k order, each 16 * code.
-__device__ __forceinline__ i32x4 unpack16x16(uint32_t lo, uint32_t hi) {
-    const uint32_t sl = lo << 4, sh = hi << 4;
-    i32x4 r;
-    r[0] = (int)(__builtin_amdgcn_perm(lo, sl, 0x05010400u) & 0xf0f0f0f0u);
-    r[1] = (int)(__builtin_amdgcn_perm(lo, sl, 0x07030602u) & 0xf0f0f0f0u);
-    r[2] = (int)(__builtin_amdgcn_perm(hi, sh, 0x05010400u) & 0xf0f0f0f0u);
-    r[3] = (int)(__builtin_amdgcn_perm(hi, sh, 0x07030602u) & 0xf0f0f0f0u);
-    return r;
-}
+// after folding round r.  (swz, unpack16x16: w4a8_common.h.)
 
 template <int MT, int NB, int WAVES, int SB, int G>
 __global__ __launch_bounds__(WAVES * 64) void w4a8_mfma_kernel(
@@ -1272,10 +1251,15 @@ int launch_linear_w4a8_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t 
                              float* xs_out, hipStream_t st) {
     if (M == 0) return FNI8_OK;
     // One token: the streaming kernel with the quantization fused.  From two
-    // tokens on, a quantize launch plus the MFMA decode kernel is faster than
-    // the VALU-bound stream kernel (Qwen3-8B shapes at 4 tokens: 9.7 / 8.0 /
-    // 17.7 / 16.0 us against 12.0 / 9.2 / 26.9 / 20.9 us).
-    if (M > 1 && G >= 64 && K % 256 == 0) return 1;
+    // tokens on, the MFMA decode kernel beats the VALU-bound stream kernel
+    // (Qwen3-8B shapes at 4 tokens, with a quantize launch in front: 9.7 / 8.0
+    // / 17.7 / 16.0 us against 12.0 / 9.2 / 26.9 / 20.9 us); up to 4 tokens it
+    // runs with the quantization fused (w4a8_fused.hip), else after a quantize
+    // launch (the caller's, on a 1).
+    if (M > 1 && G >= 64 && K % 256 == 0)
+        return M <= 4 ? launch_linear_w4a8_mfma_fused(x, ldx, M, K, w, ws, N, G, bias, y, ldy,
+                                                      xq_out, xs_out, st)
+                      : 1;
     return stream_dispatch<true>(x, ldx, nullptr, M, K, w, ws, N, G, bias, y, ldy, xq_out,
                                  xs_out, st);
 }

@@ -169,6 +169,84 @@ def test_w4a8_mfma_strided_rows(pkg):
     _check(pkg, x, qt, None)
 
 
+@pytest.mark.parametrize("G", [64, 128, 256])
+@pytest.mark.parametrize("K", [1024, 2048, 3072, 4096, 6144, 8192, 10240, 12288, 16384])
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_w4a8_fused_mfma_bitexact(pkg, M, K, G):
+    """2..4 tokens: the MFMA decode kernel with the quantization fused in (one
+    launch).  Up to K = 4096 every M runs it, on four waves (K = 2048, 4096)
+    or two (K = 1024, 3072); above, 2 tokens run it at every chunk count of
+    the four-wave shape (K = 2048 * chunks: 3, 4, 6, 8) and 3-4 tokens, like
+    K = 10240, take the quantize launch plus the MFMA kernel.  xq, xs and
+    every output element against the oracle, ragged N, bias on odd M."""
+    print(f"w4a8 fused mfma M={M} K={K} G={G}", flush=True)
+    N = 72
+    qt = _w4(pkg, N, K, G, seed=M * 17 + K + G)
+    bias = torch.randn(N, device="cuda").half() if M % 2 else None
+    _check(pkg, _x(M, K, seed=M * 19 + K + G), qt, bias)
+
+
+@pytest.mark.parametrize("G", [64, 256])
+@pytest.mark.parametrize("N,K", [(4100, 4096), (4127, 2048)])
+def test_w4a8_fused_mfma_32_row_blocks(pkg, N, K, G):
+    """4 tokens with N above 4096: 32 weight rows per workgroup (two MFMA
+    blocks), N ragged so the last workgroup holds a partial block; sampled
+    columns (the last ones included) against the oracle, with bias."""
+    print(f"w4a8 fused mfma 32-row N={N} K={K} G={G}", flush=True)
+    M = 4
+    qt = _w4(pkg, N, K, G, seed=N + K + G)
+    cols = np.concatenate([np.sort(np.random.default_rng(N).choice(N - 64, 448, replace=False)),
+                           np.arange(N - 64, N)])
+    _check(pkg, _x(M, K, seed=G), qt, torch.randn(N, device="cuda").half(), cols=cols)
+
+
+@pytest.mark.parametrize("ld_pad", [64, 3])
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_w4a8_fused_mfma_wide_and_strided(pkg, M, ld_pad):
+    """The wide-N shape (N >= 16384: 32 rows, two waves, one slab per round;
+    2-3 tokens, 4 take the quantize launch) on a row view of a wider buffer.
+    A row stride that is a multiple of 8 elements stays on the fused kernel;
+    an odd one falls back to the quantize launch.  Sampled columns against the
+    oracle (rows and columns are independent)."""
+    print(f"w4a8 fused mfma wide M={M} ld_pad={ld_pad}", flush=True)
+    K, N, G = 4096, 16400, 128
+    qt = _w4(pkg, N, K, G, seed=ld_pad)
+    big = _x(M, K + ld_pad + 8, seed=ld_pad + 1)
+    x = big[:, 8:8 + K]
+    cols = np.sort(np.random.default_rng(ld_pad).choice(N, 512, replace=False))
+    cols[-1] = N - 1
+    _check(pkg, x, qt, torch.randn(N, device="cuda").half(), cols=cols)
+
+
+def test_w4a8_fused_mfma_special_rows(pkg):
+    """Zero, subnormal-only, inf, -65504 and NaN rows through the fused
+    quantization: xq and the output against the oracle (NaN where the oracle
+    has NaN, equal bits elsewhere)."""
+    K, N, G = 4096, 200, 128
+    rows = np.zeros((4, K), np.float16)
+    rows[1, 7] = 6e-8                    # subnormal only
+    rows[2, :] = np.linspace(-3, 3, K)
+    rows[2, 99] = np.inf                 # inf row: inf scale, q = 0
+    rows[3, :] = np.float16(-65504)
+    rows[3, ::3] = 2.5
+    nan_rows = np.ones((2, K), np.float16)
+    nan_rows[1, 1000] = np.nan
+    qt = _w4(pkg, N, K, G, seed=23)
+    w, ws = qt.data.cpu().numpy(), qt.scale.cpu().numpy()
+    for arr in (rows, nan_rows):
+        y, xq, xs, _ = pkg.ops.linear_with_intermediates(torch.from_numpy(arr).cuda(), qt, None)
+        q_ref, s_ref = o.quant_rowwise_f16(arr)
+        assert np.array_equal(xq.cpu().numpy(), q_ref)
+        got_s = xs.cpu().numpy()
+        assert np.array_equal(np.isnan(got_s), np.isnan(s_ref))
+        assert np.array_equal(got_s[~np.isnan(s_ref)].view(np.uint32),
+                              s_ref[~np.isnan(s_ref)].view(np.uint32))
+        want = o.gemm_w4a8(q_ref, s_ref, w, ws, G)
+        a = y.cpu().numpy()
+        assert np.array_equal(np.isnan(a), np.isnan(want))
+        assert np.array_equal(a[~np.isnan(a)].view(np.uint16), want[~np.isnan(want)].view(np.uint16))
+
+
 @pytest.mark.parametrize("N", [1, 8, 17])
 @pytest.mark.parametrize("M", [2, 9, 40])
 def test_w4a8_mfma_decode_narrow_n(pkg, M, N):
