@@ -443,6 +443,11 @@ int launch_linear_w4a8_mfma_fused(const uint16_t* x, int64_t ldx, int64_t M, int
                                   const uint8_t* w, const float* ws, int64_t N, int64_t G,
                                   const uint16_t* bias, uint16_t* y, int64_t ldy,
                                   int8_t* xq_out, float* xs_out, hipStream_t st);
+// W4A8 decode GEMM (9 <= M <= 64, wide N) with the weight rows split over the
+// waves and one shared activation tile; 1 when not taken.
+int launch_w4a8_rowblock(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                         const uint8_t* w, const float* ws, int64_t N, int64_t G,
+                         const uint16_t* bias, uint16_t* y, int64_t ldy, hipStream_t st);
 int launch_moe_route(const float* logits, int64_t ldl, int64_t T, int64_t E, int scoring,
                      const float* bias, int64_t groups, int64_t topk_group, int64_t k, int renorm,
                      float scale, uint16_t* topw, int32_t* topi, hipStream_t st);

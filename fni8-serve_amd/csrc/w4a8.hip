@@ -1204,6 +1204,10 @@ int launch_gemm_w4a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, 
                      const uint8_t* w, const float* ws, int64_t N, int64_t G,
                      const uint16_t* bias, uint16_t* y, int64_t ldy, hipStream_t st) {
     if (M == 0) return FNI8_OK;
+    if (M > 8) {  // wide N: the row-block kernel (w4a8_rowblock.hip)
+        const int rc = launch_w4a8_rowblock(xq, ldq, xs, M, K, w, ws, N, G, bias, y, ldy, st);
+        if (rc != 1) return rc;
+    }
     if (M > kMfmaMinM) {
         const int rc = mfma_dispatch(xq, ldq, xs, M, K, w, ws, N, G, bias, y, ldy, st);
         if (rc != 1) return rc;

@@ -247,6 +247,23 @@ def test_w4a8_fused_mfma_special_rows(pkg):
         assert np.array_equal(a[~np.isnan(a)].view(np.uint16), want[~np.isnan(want)].view(np.uint16))
 
 
+@pytest.mark.parametrize("G", [64, 128, 256])
+@pytest.mark.parametrize("K", [512, 1536, 4096])
+@pytest.mark.parametrize("M,N", [(9, 16400), (16, 16391), (17, 16400), (33, 16391),
+                                 (48, 16400), (64, 16391)])
+def test_w4a8_rowblock_bitexact(pkg, M, N, K, G):
+    """9..64 tokens on wide N: the row-block kernel (waves split the weight
+    rows, one shared activation tile, folds in registers).  N leaves the last
+    workgroup with waves wholly past N (16400) or a partial 16-row block
+    (16391); K = 512 is one batch, 1536 an odd number of them.  All rows,
+    sampled columns (the last 64 included) against the oracle, with bias."""
+    print(f"w4a8 rowblock M={M} N={N} K={K} G={G}", flush=True)
+    qt = _w4(pkg, N, K, G, seed=M + K + G)
+    cols = np.concatenate([np.sort(np.random.default_rng(M + K).choice(N - 64, 384, replace=False)),
+                           np.arange(N - 64, N)])
+    _check(pkg, _x(M, K, seed=M * 3 + K + G), qt, torch.randn(N, device="cuda").half(), cols=cols)
+
+
 @pytest.mark.parametrize("N", [1, 8, 17])
 @pytest.mark.parametrize("M", [2, 9, 40])
 def test_w4a8_mfma_decode_narrow_n(pkg, M, N):
