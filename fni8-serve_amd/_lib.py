@@ -32,6 +32,7 @@ SIGNATURES = {
     "fni8_gemm_w8a8_grouped": [_P, _P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _P, _P, _P],
     "fni8_moe_combine_f16": [_P, _I, _P, _P, _P, _I, _I, _P, _P],
     "fni8_gemm_w4a8": [_P, _I, _P, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P],
+    "fni8_gemm_w4a8_grouped": [_P, _P, _P, _I, _I, _P, _P, _I, _I, _I, _P, _P, _P, _P],
     "fni8_linear_w4a8_f16": [_P, _I, _I, _I, _P, _P, _I, _I, _P, _P, _I, _P, _P, _P],
     "fni8_moe_route": [_P, _I, _I, _I, _C, _P, _I, _I, _I, _C, _F, _P, _P, _P],
     "fni8_act_and_mul_f16": [_P, _I, _I, _I, _C, _P, _I, _P],

@@ -321,6 +321,28 @@ int fni8_gemm_w8a8_grouped(const int8_t* aq, const float* as, const int32_t* row
                               (hipStream_t)stream);
 }
 
+int fni8_gemm_w4a8_grouped(const int8_t* aq, const float* as, const int32_t* row_index,
+                           int64_t R_max, int64_t K, const uint8_t* w, const float* ws,
+                           int64_t E, int64_t N, int64_t G, const int32_t* seg_off,
+                           const void* bias, void* y, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(aq && as && w && ws && seg_off && y, FNI8_ERR_NULL,
+            "aq, as, w, ws, seg_off and y are required");
+    int rc = check_w4a8(R_max, K, N, G, w, ws, bias, y, N);
+    if (rc) return rc;
+    REQUIRE(E > 0 && E < 65536, FNI8_ERR_SHAPE, "E=%lld out of range", (long long)E);
+    REQUIRE(G >= 64 && K % 256 == 0 && N < (1 << 21), FNI8_ERR_SHAPE,
+            "grouped W4A8 needs G in {64, 128, 256}, K a multiple of 256 and N < 2^21 "
+            "(G=%lld K=%lld N=%lld)", (long long)G, (long long)K, (long long)N);
+    REQUIRE(aligned(aq, 16) && aligned(as, 4) && aligned(row_index, 4) && aligned(seg_off, 4),
+            FNI8_ERR_ALIGN, "aq must be 16-byte aligned; as, row_index, seg_off 4-byte aligned");
+    rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_gemm_w4a8_grouped(aq, as, row_index, R_max, K, w, ws, E, N, G, seg_off,
+                                           (const uint16_t*)bias, (uint16_t*)y,
+                                           (hipStream_t)stream);
+}
+
 int fni8_moe_combine_f16(const void* y_sorted, int64_t H, const int32_t* topi,
                          const void* topw, const int32_t* pos, int64_t T, int64_t k,
                          void* out, void* stream) {

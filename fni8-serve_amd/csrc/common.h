@@ -448,6 +448,11 @@ int launch_linear_w4a8_mfma_fused(const uint16_t* x, int64_t ldx, int64_t M, int
 int launch_w4a8_rowblock(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
                          const uint8_t* w, const float* ws, int64_t N, int64_t G,
                          const uint16_t* bias, uint16_t* y, int64_t ldy, hipStream_t st);
+// Grouped W4A8 GEMM over expert segments (K % 256 == 0, G in {64, 128, 256}).
+int launch_gemm_w4a8_grouped(const int8_t* aq, const float* as, const int32_t* row_index,
+                             int64_t R_max, int64_t K, const uint8_t* w, const float* ws,
+                             int64_t E, int64_t N, int64_t G, const int32_t* seg_off,
+                             const uint16_t* bias, uint16_t* y, hipStream_t st);
 int launch_moe_route(const float* logits, int64_t ldl, int64_t T, int64_t E, int scoring,
                      const float* bias, int64_t groups, int64_t topk_group, int64_t k, int renorm,
                      float scale, uint16_t* topw, int32_t* topi, hipStream_t st);

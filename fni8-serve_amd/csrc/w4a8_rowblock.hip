@@ -23,14 +23,21 @@
 // Activation loads for tokens past M are skipped: those tile rows hold stale
 // values whose products land in outputs that are never stored.  Weight rows
 // past N repeat row N-1 (computed, never stored).
+//
+// GROUPED: the expert-segment form of the MoE layer's projections (one launch
+// for all experts).  Segments seg_off[E+1] of sorted rows; blockIdx.x is one
+// 16*MT-row piece of one expert's segment, blockIdx.y the weight-row block;
+// sorted row r reads activation row rmap[r] (row r without a map) and its scale;
+// weights, scales and bias are stacked per expert; y is in sorted-row order.
 #include "w4a8_common.h"
 
 namespace {
 
-template <int MT, int WAVES, int SB, int G>
+template <int MT, int WAVES, int SB, int G, bool GROUPED = false>
 __global__ __launch_bounds__(WAVES * 64) void w4a8_rowblock_kernel(
-    const int8_t* __restrict__ xq, int64_t ldx, const float* __restrict__ xs, int M, int K,
-    const uint8_t* __restrict__ w, const float* __restrict__ ws, int N,
+    const int8_t* __restrict__ xq, int64_t ldx, const float* __restrict__ xs,
+    const int32_t* __restrict__ rmap, int M, int K, const uint8_t* __restrict__ w,
+    const float* __restrict__ ws, int N, int E, const int32_t* __restrict__ seg_off,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy) {
     constexpr int NT = WAVES * 64;
     constexpr int TOK = 16 * MT;
@@ -48,9 +55,26 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_rowblock_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     int8_t* xt = smem;                                     // [2][SB][XT]
     int8_t* wt = smem + 2 * SB * XT + wave * (SB * WT);    // this wave's [SB][WT]
-    const int n0 = blockIdx.x * (16 * WAVES) + 16 * wave;  // the wave's first weight row
     const int nb = (K >> 8) / SB;                          // batches (the launcher makes it exact)
     const int ng = K / G;
+    int r0 = 0, rblk = blockIdx.x;
+    if constexpr (GROUPED) {
+        // every wave finds the same tile; past the last tile the whole
+        // workgroup leaves before any barrier
+        int e, r1;
+        if (!fni8::find_group_tile(seg_off, E, TOK, blockIdx.x, M, e, r0, r1)) return;
+        M = r1 - r0;
+        rblk = blockIdx.y;
+        w += (int64_t)e * N * (K >> 1);
+        ws += (int64_t)e * N * ng;
+        if (bias != nullptr) bias += (int64_t)e * N;
+    }
+    // activation row of the tile's token t (t < M)
+    auto src_row = [&](int t) -> int {
+        if constexpr (GROUPED) return rmap != nullptr ? rmap[r0 + t] : r0 + t;
+        return t;
+    };
+    const int n0 = rblk * (16 * WAVES) + 16 * wave;  // the wave's first weight row
     const int rq = lane >> 3, c = lane & 7, r = lane & 15, g = lane >> 4;
 
     // weight load lanes: row h*8 + rq of the wave's block, 16-byte chunk c
@@ -73,7 +97,7 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_rowblock_kernel(
         const int q = i * NT + tid;
         const int tok = q >> 4, hf = (q >> 3) & 1, cc = q & 7;
         xlive[i] = q < XCH && tok < M;
-        xsrc[i] = xq + (int64_t)(tok < M ? tok : 0) * ldx + hf * 128 + cc * 16;
+        xsrc[i] = xq + (int64_t)src_row(tok < M ? tok : 0) * ldx + hf * 128 + cc * 16;
         const int row = hf * TOK + (tok < TOK ? tok : 0);
         xoff[i] = row * 128 + swz(row, cc);
     }
@@ -177,9 +201,9 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_rowblock_kernel(
             for (int i = 0; i < 4; i++) {
                 const int m = mt * 16 + 4 * g + i;
                 if (m < M) {
-                    float v = accf[mt][i] * xs[m];
+                    float v = accf[mt][i] * xs[src_row(m)];
                     if (bias) v = v + fni8::h2f(bias[n]);
-                    y[(int64_t)m * ldy + n] = fni8::f2h(v);
+                    y[(int64_t)(r0 + m) * ldy + n] = fni8::f2h(v);
                 }
             }
     }
@@ -211,8 +235,8 @@ int rowblock_launch(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, i
             }
         }
         const dim3 grid((unsigned)((N + 16 * WAVES - 1) / (16 * WAVES)));
-        hipLaunchKernelGGL(kern, grid, dim3(WAVES * 64), lds, st, xq, ldq, xs, (int)M, (int)K, w,
-                           ws, (int)N, bias, y, ldy);
+        hipLaunchKernelGGL(kern, grid, dim3(WAVES * 64), lds, st, xq, ldq, xs, nullptr, (int)M,
+                           (int)K, w, ws, (int)N, 0, nullptr, bias, y, ldy);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) {
             fni8h::set_error_detail("w4a8 row-block launch: %s", hipGetErrorString(e));
@@ -220,6 +244,53 @@ int rowblock_launch(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, i
         }
         return FNI8_OK;
     }
+}
+
+// Grouped form: activation rows of stride K, y of stride N; the grid's x
+// dimension bounds the segment tiles (sum over experts of ceil(len / (16*MT))
+// <= R_max / (16*MT) + E), its y dimension the weight-row blocks.
+template <int MT, int WAVES, int SB, int G>
+int rowblock_grouped_launch(const int8_t* aq, const float* as, const int32_t* rmap,
+                            int64_t R_max, int64_t K, const uint8_t* w, const float* ws,
+                            int64_t E, int64_t N, const int32_t* seg_off, const uint16_t* bias,
+                            uint16_t* y, hipStream_t st) {
+    constexpr size_t lds = kRowblockLds<MT, WAVES, SB>;
+    static_assert(lds <= kLdsLimit, "LDS budget");
+    auto kern = &w4a8_rowblock_kernel<MT, WAVES, SB, G, true>;
+    if constexpr (lds > 64 * 1024) {
+        static const bool ok = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   (int)lds) == hipSuccess;
+        if (!ok) {
+            fni8h::set_error_detail("w4a8 grouped: cannot raise the LDS limit to %zu bytes", lds);
+            return FNI8_ERR_LAUNCH;
+        }
+    }
+    const dim3 grid((unsigned)((R_max + 16 * MT - 1) / (16 * MT) + E),
+                    (unsigned)((N + 16 * WAVES - 1) / (16 * WAVES)));
+    hipLaunchKernelGGL(kern, grid, dim3(WAVES * 64), lds, st, aq, K, as, rmap, (int)R_max,
+                       (int)K, w, ws, (int)N, (int)E, seg_off, bias, y, N);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fni8h::set_error_detail("w4a8 grouped launch: %s", hipGetErrorString(e));
+        return FNI8_ERR_LAUNCH;
+    }
+    return FNI8_OK;
+}
+
+template <int G>
+int grouped_by_tile(const int8_t* aq, const float* as, const int32_t* rmap, int64_t R_max,
+                    int64_t K, const uint8_t* w, const float* ws, int64_t E, int64_t N,
+                    const int32_t* seg_off, const uint16_t* bias, uint16_t* y, hipStream_t st) {
+    // segment tiles of 16, 32 or 64 rows by the mean rows per expert; two
+    // slabs per batch where K allows
+    const double avg = (double)R_max / (double)E;
+    const bool sb2 = (K >> 8) % 2 == 0;
+#define FNI8_W4G(MTV, WV)                                                                             return sb2 ? rowblock_grouped_launch<MTV, WV, 2, G>(aq, as, rmap, R_max, K, w, ws, E, N,                                                             seg_off, bias, y, st)                                   : rowblock_grouped_launch<MTV, WV, 1, G>(aq, as, rmap, R_max, K, w, ws, E, N,                                                             seg_off, bias, y, st)
+    if (avg <= 16.0) FNI8_W4G(1, 2);
+    if (avg <= 32.0) FNI8_W4G(2, 4);
+    FNI8_W4G(4, 4);
+#undef FNI8_W4G
 }
 
 }  // namespace
@@ -260,6 +331,20 @@ int launch_w4a8_rowblock(const int8_t* xq, int64_t ldq, const float* xs, int64_t
     }
 #undef FNI8_W4RB_MT
 #undef FNI8_W4RB
+}
+
+// Grouped W4A8 over expert segments (K a multiple of 256, G in {64, 128, 256}:
+// the caller checks).
+int launch_gemm_w4a8_grouped(const int8_t* aq, const float* as, const int32_t* row_index,
+                             int64_t R_max, int64_t K, const uint8_t* w, const float* ws,
+                             int64_t E, int64_t N, int64_t G, const int32_t* seg_off,
+                             const uint16_t* bias, uint16_t* y, hipStream_t st) {
+    if (R_max == 0) return FNI8_OK;
+    switch (G) {
+        case 64: return grouped_by_tile<64>(aq, as, row_index, R_max, K, w, ws, E, N, seg_off, bias, y, st);
+        case 128: return grouped_by_tile<128>(aq, as, row_index, R_max, K, w, ws, E, N, seg_off, bias, y, st);
+        default: return grouped_by_tile<256>(aq, as, row_index, R_max, K, w, ws, E, N, seg_off, bias, y, st);
+    }
 }
 
 }  // namespace fni8h

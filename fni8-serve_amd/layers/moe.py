@@ -1,4 +1,4 @@
-"""Sparse MoE FFN with the expert loop replaced by grouped W8A8 GEMMs.
+"""Sparse MoE FFN with the expert loop replaced by grouped W8A8 (or W4A8) GEMMs.
 
 Same constructor and routing as fni8serve/models/moe.py:25-113 (softmax or
 sigmoid scoring, optional group-limited top-k, renormalisation, routed
@@ -25,13 +25,16 @@ Because quantization is row-local and the GEMM is exact, every int8 row, int32
 accumulator and fp16 expert output equals what the per-expert loop computes.
 CPU inputs run the reference's loop unchanged.
 
-Experts of another scheme (per_group_i4 int4 weights, as the reference's
-converter writes for weight_bits=4, fni8serve/convert.py:130-131) keep their
-own GatedMLP modules (moe.py:56).  On the GPU they run on the same device
+Experts of per_group_i4 int4 weights (as the reference's converter writes for
+weight_bits=4, fni8serve/convert.py:130-131) run the same chain on the grouped
+W4A8 GEMM when every expert of a projection shares one layout (shape, group
+size 64-256, K a multiple of 256): again no host sync, and the arithmetic of
+the per-expert W4A8 linears.  Other experts (mixed schemes or layouts) keep
+their own GatedMLP modules (moe.py:56): on the GPU they run on the same device
 routing and sort, then each non-empty expert's sorted rows go through its
-GatedMLP (the W4A8 kernels) and the same combine: one host read of the segment
-offsets per layer instead of the reference's two syncs per expert, and the
-same per-expert arithmetic and index_add_ order.
+GatedMLP and the same combine -- one host read of the segment offsets per
+layer instead of the reference's two syncs per expert, and the same
+per-expert arithmetic and index_add_ order.
 """
 from __future__ import annotations
 
@@ -43,6 +46,24 @@ from .. import ops
 from ..qtensor import QTensor
 from .activation import fused_act, get_act_and_mul
 from .mlp import GatedMLP
+
+
+def _w4_stackable(qs: list[QTensor]) -> bool:
+    """True when every QTensor is a per_group_i4 int4 weight of one shape and
+    group size that the grouped W4A8 kernel takes (G in 64..256, K a multiple
+    of 256, fp32 scales)."""
+    q0 = qs[0]
+    if q0.scheme != "per_group_i4" or q0.data.dim() != 2:
+        return False
+    N, Kh = q0.data.shape
+    G = q0.group_size
+    if G not in ops.W4_GROUPED_GROUPS or (2 * Kh) % 256 or (2 * Kh) % G:
+        return False
+    return all(q.scheme == "per_group_i4" and q.codebook == "int4" and q.group_size == G
+               and q.data.dtype == torch.uint8 and tuple(q.data.shape) == (N, Kh)
+               and q.scale is not None and q.scale.dtype == torch.float32
+               and q.scale.numel() == N * (2 * Kh // G) and q.data.device == q0.data.device
+               for q in qs)
 
 
 class SparseMoE(nn.Module):
@@ -73,9 +94,32 @@ class SparseMoE(nn.Module):
         self.shared_gate = (nn.Parameter(shared_expert_gate)
                             if shared_expert_gate is not None else None)
         self.grouped = all(q.scheme == "per_row_i8" for q in gu + dn)
+        self.grouped_w4 = not self.grouped and _w4_stackable(gu) and _w4_stackable(dn)
+        if self.grouped_w4:
+            # per_group_i4 int4 experts of one layout per projection: stacked
+            # packed weights [E, N, K/2] and group scales [E, N, K/G] for the
+            # grouped W4A8 kernel; the per-expert modules keep views
+            self.g_gate_up, self.g_down = gu[0].group_size, dn[0].group_size
+            for name, qs in (("gate_up", gu), ("down", dn)):
+                N, Kh = qs[0].data.shape
+                G = qs[0].group_size
+                self.register_buffer(f"w_{name}", torch.stack([q.data for q in qs]).contiguous(),
+                                     persistent=False)
+                self.register_buffer(
+                    f"s_{name}",
+                    torch.stack([q.scale.reshape(N, 2 * Kh // G) for q in qs]).contiguous(),
+                    persistent=False)
+            self.experts = nn.ModuleList([
+                GatedMLP(QTensor(self.w_gate_up[e], self.s_gate_up[e], scheme="per_group_i4",
+                                 group_size=self.g_gate_up, codebook="int4"),
+                         QTensor(self.w_down[e], self.s_down[e], scheme="per_group_i4",
+                                 group_size=self.g_down, codebook="int4"), act=act)
+                for e in range(self.num_experts)])
+            return
         if not self.grouped:
-            # per_group_i4 (or mixed) experts: one GatedMLP per expert on its own
-            # QTensors, as the reference builds them (moe.py:56)
+            # mixed experts, or int4 layouts the grouped kernel does not take:
+            # one GatedMLP per expert on its own QTensors, as the reference
+            # builds them (moe.py:56)
             self.experts = nn.ModuleList([GatedMLP(g_, d_, act=act) for g_, d_ in experts])
             return
         # Stacked expert weights [E, N, K] / scales [E, N] for the grouped kernel;
@@ -156,6 +200,24 @@ class SparseMoE(nn.Module):
         y = ops.gemm_w8a8_grouped(aq, as_, self.w_down, self.s_down, seg_off, R)
         return ops.moe_combine(y, topi, topw, pos)
 
+    def experts_grouped_w4(self, xf: torch.Tensor, topw: torch.Tensor, topi: torch.Tensor):
+        """int4 experts in two grouped W4A8 launches; returns out [T, H].  The same
+        chain as experts_grouped: per-token quantization once, the gate_up
+        segments with rows gathered by token, the fused activation and
+        quantization of the sorted rows, the down segments, the combine."""
+        R = xf.shape[0] * self.top_k
+        seg_off, row_token, pos = ops.moe_sort(topi, self.num_experts)
+        xq, xs = ops.quantize_rowwise(xf)
+        h = ops.gemm_w4a8_grouped(xq, xs, self.w_gate_up, self.s_gate_up, self.g_gate_up,
+                                  seg_off, R, row_index=row_token)
+        act = fused_act(self.act_fn)
+        if act is not None:
+            aq, as_ = ops.act_and_mul_quant(h, act)
+        else:
+            aq, as_ = ops.quantize_rowwise(self.act_fn(h))
+        y = ops.gemm_w4a8_grouped(aq, as_, self.w_down, self.s_down, self.g_down, seg_off, R)
+        return ops.moe_combine(y, topi, topw, pos)
+
     def experts_sorted(self, xf: torch.Tensor, topw: torch.Tensor, topi: torch.Tensor):
         """Experts that are not per_row_i8 (the W4A8 path): device sort, one host
         read of the segment offsets, each non-empty expert's GatedMLP on its
@@ -188,8 +250,12 @@ class SparseMoE(nn.Module):
         xf = x.reshape(-1, H)
         topw, topi = self.route(xf)
         if xf.is_cuda:
-            out = (self.experts_grouped(xf, topw, topi) if self.grouped
-                   else self.experts_sorted(xf, topw, topi))
+            if self.grouped:
+                out = self.experts_grouped(xf, topw, topi)
+            elif self.grouped_w4:
+                out = self.experts_grouped_w4(xf, topw, topi)
+            else:
+                out = self.experts_sorted(xf, topw, topi)
         else:
             out = self._experts_loop(xf, topw, topi)
         if self.shared is not None:

@@ -279,6 +279,50 @@ def gemm_w8a8_grouped(aq: torch.Tensor, as_: torch.Tensor, w: torch.Tensor, ws: 
     return (y, acc) if want_acc else y
 
 
+W4_GROUPED_GROUPS = (64, 128, 256)
+
+
+def gemm_w4a8_grouped(aq: torch.Tensor, as_: torch.Tensor, w: torch.Tensor, ws: torch.Tensor,
+                      G: int, seg_off: torch.Tensor, rows: int,
+                      row_index: torch.Tensor | None = None,
+                      bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Grouped W4A8 GEMM over expert segments (per_group_i4 int4 experts).
+    aq int8 [A, K], as_ fp32 [A]; w uint8 [E, N, K/2]; ws fp32 [E, N, K/G];
+    seg_off int32 [E+1]; row_index int32 [rows] or None -> y fp16 [rows, N] in
+    sorted-row order.  G in (64, 128, 256), K a multiple of 256."""
+    if aq.dtype != torch.int8 or aq.dim() != 2 or not aq.is_contiguous():
+        raise ValueError("aq must be a contiguous int8 [rows, K] tensor")
+    if w.dtype != torch.uint8 or w.dim() != 3 or not w.is_contiguous():
+        raise ValueError("w must be a contiguous uint8 [E, N, K/2] tensor")
+    E, N, Kh = w.shape
+    K = 2 * Kh
+    if aq.shape[1] != K:
+        raise ValueError(f"in_features mismatch: {aq.shape[1]} vs {K}")
+    if G not in W4_GROUPED_GROUPS or K % 256:
+        raise ValueError(f"grouped W4A8 needs G in {W4_GROUPED_GROUPS} and K a multiple of 256 "
+                         f"(G={G}, K={K})")
+    if ws.dtype != torch.float32 or ws.shape != (E, N, K // G) or not ws.is_contiguous():
+        raise ValueError("ws must be a contiguous fp32 [E, N, K/G] tensor")
+    if as_.dtype != torch.float32 or as_.numel() != aq.shape[0] or not as_.is_contiguous():
+        raise ValueError("as_ must be a contiguous fp32 tensor with one entry per row of aq")
+    if seg_off.dtype != torch.int32 or seg_off.numel() != E + 1:
+        raise ValueError("seg_off must be int32 [E+1]")
+    if row_index is not None and (row_index.dtype != torch.int32 or row_index.numel() < rows):
+        raise ValueError("row_index must be int32 with at least `rows` entries")
+    if row_index is None and aq.shape[0] < rows:
+        raise ValueError("aq has fewer rows than `rows`")
+    if bias is not None and (bias.dtype != _f16 or bias.shape != (E, N)):
+        raise ValueError("bias must be fp16 [E, N]")
+    dev = _require_cuda("gemm_w4a8_grouped", aq, as_, w, ws, seg_off, row_index, bias)
+    y = torch.empty((rows, N), dtype=_f16, device=dev)
+    if rows:
+        with torch.cuda.device(dev):
+            _lib.call("fni8_gemm_w4a8_grouped", _ptr(aq), _ptr(as_), _ptr(row_index), rows, K,
+                      _ptr(w), _ptr(ws), E, N, G, _ptr(seg_off), _ptr(bias), _ptr(y),
+                      _stream(dev))
+    return y
+
+
 def moe_combine(y_sorted: torch.Tensor, topi: torch.Tensor, topw: torch.Tensor,
                 pos: torch.Tensor) -> torch.Tensor:
     """out[t] = sum over slots (ascending expert id) of fp16(y_sorted[pos[t, j]] * topw[t, j]),

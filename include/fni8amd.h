@@ -148,6 +148,29 @@ int fni8_gemm_w8a8_grouped(const int8_t* aq, const float* as, const int32_t* row
                            void* y, int32_t* acc_out, void* stream);
 
 /*
+ * Grouped W4A8 GEMM over expert segments: all per_group_i4 experts'
+ * `gemm_w4a8` calls of one projection in one launch (replaces the expert
+ * loop's linears on int4 experts, fni8serve/models/moe.py:104 via
+ * layers/mlp.py:39-40; experts of any QTensor scheme, moe.py:56, and the
+ * converter's per_group_i4 experts, convert.py:130-131).
+ *   aq, as     int8 [rows, K] (row stride K, 16-byte aligned) and fp32 [rows]
+ *   row_index  int32 [R] or NULL: sorted row r reads activation row
+ *              row_index[r]; NULL reads row r
+ *   w, ws      uint8 [E, N, K/2] (packed as in fni8_gemm_w4a8, 16-byte aligned)
+ *              and fp32 [E, N, K/G]: stacked expert weights and group scales
+ *   G          64, 128 or 256; K a multiple of 256; N < 2^21
+ *   seg_off    int32 [E + 1] from fni8_moe_sort; R = seg_off[E] on the device,
+ *              R_max bounds it
+ *   bias       fp16 [E, N] or NULL
+ *   y          fp16 [R_max, N] in sorted-row order (rows >= R are not written)
+ * Per output element the arithmetic of fni8_gemm_w4a8.
+ */
+int fni8_gemm_w4a8_grouped(const int8_t* aq, const float* as, const int32_t* row_index,
+                           int64_t R_max, int64_t K, const uint8_t* w, const float* ws,
+                           int64_t E, int64_t N, int64_t G, const int32_t* seg_off,
+                           const void* bias, void* y, void* stream);
+
+/*
  * Weighted combine of expert outputs (replaces moe.py:105's
  * `out.index_add_(0, tok_idx, contrib * topw[tok_idx, slot])` over the
  * expert loop): out[t] = sum over the token's slots, in ascending expert id,

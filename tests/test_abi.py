@@ -75,6 +75,23 @@ def test_argument_errors_return_before_any_launch(lib):
     assert rc == -2
 
 
+def test_grouped_w4a8_argument_errors(lib):
+    P = ctypes.c_void_p
+    fake = P(0x1000)  # never dereferenced: every call fails its argument checks
+    args = lambda aq=fake, K=512, E=4, G=128: (aq, fake, None, 8, K, fake, fake, E, 64, G, fake,
+                                               None, fake, None)
+    rc = lib.fni8_gemm_w4a8_grouped(*args(G=32))   # group 32: the dense kernels only
+    assert rc == -2 and b"grouped W4A8" in lib.fni8_last_error()
+    rc = lib.fni8_gemm_w4a8_grouped(*args(K=384))  # K not a multiple of 256
+    assert rc == -2 and b"multiple of 256" in lib.fni8_last_error()
+    assert lib.fni8_gemm_w4a8_grouped(*args(E=0)) == -2
+    assert lib.fni8_gemm_w4a8_grouped(*args(aq=P(0x1008))) == -3  # aq 16-byte alignment
+    assert lib.fni8_gemm_w4a8_grouped(*args(K=200)) == -2          # K % G
+    rc = lib.fni8_gemm_w4a8_grouped(None, fake, None, 8, 512, fake, fake, 4, 64, 128, fake, None,
+                                    fake, None)
+    assert rc == -1
+
+
 def test_act_and_norm_argument_errors(lib):
     fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call fails its checks
     F = ctypes.c_float

@@ -286,19 +286,24 @@ def test_w4a8_tile8_group256_bitexact(pkg, M, N, K):
     _check(pkg, _x(M, K, seed=M * 7 + K), qt, bias)
 
 
-@pytest.mark.parametrize("T", [3, 40])
-def test_sparse_moe_w4_experts_against_oracle(pkg, T):
+@pytest.mark.parametrize("T,G,H,I", [(3, 64, 512, 256), (40, 64, 512, 256),
+                                     (200, 128, 1024, 768), (24, 32, 512, 256)])
+def test_sparse_moe_w4_experts_against_oracle(pkg, T, G, H, I):
     """SparseMoE over per_group_i4 int4 experts (the reference builds experts
     from any QTensor scheme, fni8serve/models/moe.py:56; its converter writes
     per_group_i4 for weight_bits=4, convert.py:130-131): the layer output bit for
     bit against the oracle's sort, per-expert W4A8 chain (gate_up, silu-and-mul,
-    down) and combine, on the same routing.  T = 3 leaves every expert below the
-    fused activation's row threshold, T = 40 puts several experts above it."""
-    E, H, I, k, G = 16, 512, 256, 4, 64
+    down) and combine, on the same routing.  G = 64 and 128 run the grouped
+    W4A8 GEMM (16-row segment tiles at T = 3 and 40, 64-row ones at T = 200,
+    where down's K = 768 is an odd number of slabs); G = 32 keeps the per-expert
+    modules."""
+    print(f"w4 moe T={T} G={G}", flush=True)
+    E, k = 16, 4
     experts = [(_w4(pkg, 2 * I, H, G, seed=e), _w4(pkg, H, I, G, seed=100 + e)) for e in range(E)]
     g = torch.Generator(device="cuda").manual_seed(T)
     gate = (torch.randn(E, H, device="cuda", generator=g) * 0.05).half()
     moe = pkg.SparseMoE(gate=gate, experts=experts, top_k=k, norm_topk_prob=True)
+    assert moe.grouped_w4 == (G >= 64)
     x = _x(T, H, seed=T + 7).reshape(1, T, H)
     out = moe(x)
     topw, topi = moe.route(x.reshape(-1, H))
@@ -317,3 +322,83 @@ def test_sparse_moe_w4_experts_against_oracle(pkg, T):
         ys[lo:hi] = yd
     want = o.moe_combine_f16(ys, topi.cpu().numpy(), topw.cpu().numpy(), pos)
     assert np.array_equal(out.reshape(T, H).cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("G", [64, 128, 256])
+@pytest.mark.parametrize("K", [768, 1024])
+@pytest.mark.parametrize("per_expert", [1, 20, 60])
+def test_w4a8_grouped_gemm_bitexact(pkg, per_expert, K, G):
+    """The grouped W4A8 GEMM against the oracle expert by expert: ragged
+    segments (one expert empty), 16-, 32- and 64-row segment tiles (mean rows
+    per expert 1, 20, 60), K = 768 (odd slab count) and 1024, activation rows
+    gathered through a row map, bias, and `rows` beyond the sorted rows (those
+    are not written)."""
+    print(f"w4a8 grouped per_expert={per_expert} K={K} G={G}", flush=True)
+    E, N = 8, 200
+    rng = np.random.default_rng(per_expert + K + G)
+    lens = rng.integers(0, 2 * per_expert + 1, E)
+    lens[1] = 0
+    lens[0] = max(lens[0], 1)
+    R = int(lens.sum())
+    seg = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    A = R + 5
+    rmap = rng.integers(0, A, R + 7).astype(np.int32)
+    xq = rng.integers(-127, 128, (A, K)).astype(np.int8)
+    xs = rng.uniform(0.001, 0.05, A).astype(np.float32)
+    qts = [_w4(pkg, N, K, G, seed=e * 13 + K + G) for e in range(E)]
+    w = torch.stack([q.data for q in qts]).contiguous()
+    ws = torch.stack([q.scale for q in qts]).contiguous()
+    bias = torch.randn(E, N, device="cuda").half()
+    y = pkg.ops.gemm_w4a8_grouped(torch.from_numpy(xq).cuda(), torch.from_numpy(xs).cuda(), w, ws,
+                                  G, torch.from_numpy(seg).cuda(), R + 7,
+                                  row_index=torch.from_numpy(rmap).cuda(), bias=bias)
+    got = y.cpu().numpy()
+    wn, wsn, bn = w.cpu().numpy(), ws.cpu().numpy(), bias.cpu().numpy()
+    for e in range(E):
+        lo, hi = int(seg[e]), int(seg[e + 1])
+        if hi == lo:
+            continue
+        rows = rmap[lo:hi]
+        want = o.gemm_w4a8(xq[rows], xs[rows], wn[e], wsn[e], G, bias=bn[e])
+        assert np.array_equal(got[lo:hi].view(np.uint16), want.view(np.uint16)), f"expert {e}"
+
+
+@pytest.mark.parametrize("T", [4, 40])
+def test_sparse_moe_w4_graph_capture(pkg, T):
+    """The int4 expert layer on the grouped W4A8 GEMM has no host sync, so it
+    is captured in one HIP graph; each replay on new inputs equals the eager
+    forward bit for bit (the reference declines MoE layers for capture,
+    fni8serve/engine/cuda_graph.py:190-191)."""
+    print(f"w4 moe graph T={T}", flush=True)
+    E, H, I, k, G = 16, 512, 256, 4, 64
+    experts = [(_w4(pkg, 2 * I, H, G, seed=e), _w4(pkg, H, I, G, seed=100 + e)) for e in range(E)]
+    g = torch.Generator(device="cuda").manual_seed(T)
+    gate = (torch.randn(E, H, device="cuda", generator=g) * 0.05).half()
+    moe = pkg.SparseMoE(gate=gate, experts=experts, top_k=k, norm_topk_prob=True)
+    assert moe.grouped_w4
+    x_static = _x(T, H, seed=T + 3).reshape(1, T, H)
+    with torch.inference_mode():
+        eager0 = moe(x_static).clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                moe(x_static)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y_static = moe(x_static)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y_static, eager0)
+        for rep in range(3):
+            x_new = _x(T, H, seed=T * 10 + rep).reshape(1, T, H)
+            x_static.copy_(x_new)
+            y_static.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            want = moe(x_new)
+            torch.cuda.synchronize()
+            assert torch.isfinite(want).all()
+            assert torch.equal(y_static, want), rep
