@@ -436,7 +436,11 @@ def moe_layer_section(pkg, wl, device, route_ts=(1, 16, 256, 4096), layer_ts=(1,
                    router kernel, on the same fp32 logits (device time)
       layer        forward() eager against the same forward captured in one
                    HIP graph and replayed: wall time per call, host included,
-                   and device time of back-to-back calls"""
+                   and device time of back-to-back calls
+      w4_layer     the same layer on per_group_i4 int4 experts (G = 128): the
+                   grouped W4A8 path against the per-expert path it replaces
+                   (a host read of the segment offsets, then one GatedMLP per
+                   non-empty expert), wall time per eager call"""
     E, k, H, I = (wl.MOE[n] for n in ("experts", "top_k", "hidden", "inter"))
     g = torch.Generator(device=device).manual_seed(77)
 
@@ -486,6 +490,42 @@ def moe_layer_section(pkg, wl, device, route_ts=(1, 16, 256, 4096), layer_ts=(1,
                 "wall_speedup": round(w_eager / w_graph, 2),
                 "eager_device": round(d_eager * 1e6, 1), "graph_device": round(d_graph * 1e6, 1)}
             del graph
+    del moe
+
+    def q4(n, kk, G=128):
+        codes = torch.randint(-8, 8, (n, kk), device=device, generator=g)
+        packed = ((codes[:, 0::2] & 0xF) | ((codes[:, 1::2] & 0xF) << 4)).to(torch.uint8)
+        scale = torch.rand(n, kk // G, device=device, generator=g) * 0.002 + 1e-4
+        return pkg.QTensor(packed.contiguous(), scale.contiguous(), scheme="per_group_i4",
+                           group_size=G, codebook="int4")
+
+    moe4 = pkg.SparseMoE(gate=(torch.randn(E, H, device=device, generator=g) * 0.05).half(),
+                         experts=[(q4(2 * I, H), q4(H, I)) for _ in range(E)], top_k=k)
+    out["w4_layer_us"] = {}
+
+    def wall_n(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / reps
+
+    with torch.inference_mode():
+        for T in (1, 16, 256, 4096):
+            x = (torch.randn(1, T, H, device=device, generator=g) * 0.5).half()
+            xf = x.reshape(-1, H)
+
+            def per_expert():
+                topw, topi = moe4.route(xf)
+                return moe4.experts_sorted(xf, topw, topi)
+
+            reps = 50 if T <= 256 else 10
+            t_g, t_p = wall_n(lambda: moe4(x), reps), wall_n(per_expert, reps)
+            out["w4_layer_us"][f"T{T}"] = {"grouped_wall": round(t_g * 1e6, 1),
+                                           "per_expert_wall": round(t_p * 1e6, 1),
+                                           "speedup": round(t_p / t_g, 2)}
     return out
 
 
