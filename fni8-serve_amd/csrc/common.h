@@ -453,6 +453,11 @@ int launch_gemm_w4a8_grouped(const int8_t* aq, const float* as, const int32_t* r
                              int64_t R_max, int64_t K, const uint8_t* w, const float* ws,
                              int64_t E, int64_t N, int64_t G, const int32_t* seg_off,
                              const uint16_t* bias, uint16_t* y, hipStream_t st);
+// The W4A8 tile kernel in its expert-segment form (128-row segment tiles).
+int launch_w4a8_tile_grouped(const int8_t* aq, const float* as, const int32_t* row_index,
+                             int64_t R_max, int64_t K, const uint8_t* w, const float* ws,
+                             int64_t E, int64_t N, int64_t G, const int32_t* seg_off,
+                             const uint16_t* bias, uint16_t* y, hipStream_t st);
 int launch_moe_route(const float* logits, int64_t ldl, int64_t T, int64_t E, int scoring,
                      const float* bias, int64_t groups, int64_t topk_group, int64_t k, int renorm,
                      float scale, uint16_t* topw, int32_t* topi, hipStream_t st);

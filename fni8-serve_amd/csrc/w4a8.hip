@@ -601,10 +601,15 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_mfma_kernel(
 // accumulators; after the last step of a group every accumulator is folded
 // into its fp32 sum with the group scale of its column and reset.  The next
 // step's global loads are in flight during the current step's MFMAs.
-template <int BM, int BN, int G>
+// GROUPED: the expert-segment form (the MoE layer's projections, one launch):
+// blockIdx.x is one BM-row tile of one expert's sorted segment, blockIdx.y the
+// column tile; sorted row r reads activation row rmap[r] (row r without a map)
+// and its scale; weights, scales and bias are stacked per expert.
+template <int BM, int BN, int G, bool GROUPED = false>
 __global__ __launch_bounds__(256) void w4a8_tile_kernel(
-    const int8_t* __restrict__ xq, int64_t ldq, const float* __restrict__ xs, int M, int K,
-    const uint8_t* __restrict__ w, const float* __restrict__ ws, int N,
+    const int8_t* __restrict__ xq, int64_t ldq, const float* __restrict__ xs,
+    const int32_t* __restrict__ rmap, int M, int K, const uint8_t* __restrict__ w,
+    const float* __restrict__ ws, int N, int E, const int32_t* __restrict__ seg_off,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy) {
     constexpr int NT = 256;
     constexpr int KS = G < 128 ? G : 128;   // codes per K-step
@@ -618,9 +623,27 @@ __global__ __launch_bounds__(256) void w4a8_tile_kernel(
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
     const int ng = K / G;
     const int nsteps = K / KS;
+    // output rows [m0, mend)
+    int m0 = blockIdx.y * BM, mend = M, n0 = blockIdx.x * BN;
+    if constexpr (GROUPED) {
+        // every wave finds the same tile; past the last tile the whole
+        // workgroup leaves before any barrier
+        int e, r0, r1;
+        if (!fni8::find_group_tile(seg_off, E, BM, blockIdx.x, M, e, r0, r1)) return;
+        m0 = r0;
+        mend = r1;
+        n0 = blockIdx.y * BN;
+        w += (int64_t)e * N * (K / 2);
+        ws += (int64_t)e * N * ng;
+        if (bias != nullptr) bias += (int64_t)e * N;
+    }
+    // activation row of output row r
+    auto src_row = [&](int r) -> int {
+        if constexpr (GROUPED) return rmap != nullptr ? rmap[r] : r;
+        return r;
+    };
 
     const int8_t* asrc[A_CH];
     const uint8_t* bsrc[B_CH];
@@ -628,8 +651,8 @@ __global__ __launch_bounds__(256) void w4a8_tile_kernel(
     for (int i = 0; i < A_CH; i++) {
         const int c = (tid + i * NT) % A_TOT;  // threads past the step's chunks repeat one
         int mr = m0 + c / (KS / 16);
-        mr = mr < M ? mr : M - 1;
-        asrc[i] = xq + (int64_t)mr * ldq + (c % (KS / 16)) * 16;
+        mr = mr < mend ? mr : mend - 1;
+        asrc[i] = xq + (int64_t)src_row(mr) * ldq + (c % (KS / 16)) * 16;
     }
 #pragma unroll
     for (int i = 0; i < B_CH; i++) {
@@ -738,8 +761,8 @@ __global__ __launch_bounds__(256) void w4a8_tile_kernel(
 #pragma unroll
         for (int r = 0; r < 16; r++) {
             const int mr = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            if (mr >= M) continue;
-            const float asc = xs[mr];
+            if (mr >= mend) continue;
+            const float asc = xs[src_row(mr)];
 #pragma unroll
             for (int j = 0; j < FN; j++) {
                 const int n = n0 + wn * WTN + j * 32 + (lane & 31);
@@ -970,9 +993,24 @@ int tile_launch(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64
                 int64_t ldy, hipStream_t st) {
     constexpr int BM = 128, BN = 128;
     const dim3 grid((unsigned)((N + BN - 1) / BN), (unsigned)((M + BM - 1) / BM));
-    hipLaunchKernelGGL((w4a8_tile_kernel<BM, BN, G>), grid, dim3(256), 0, st, xq, ldq, xs, (int)M,
-                       (int)K, w, ws, (int)N, bias, y, ldy);
+    hipLaunchKernelGGL((w4a8_tile_kernel<BM, BN, G>), grid, dim3(256), 0, st, xq, ldq, xs, nullptr,
+                       (int)M, (int)K, w, ws, (int)N, 0, nullptr, bias, y, ldy);
     return launch_error("w4a8 tile");
+}
+
+// Grouped form: activation rows of stride K, y of stride N; the grid's x
+// dimension bounds the segment tiles (sum over experts of ceil(len / 128) <=
+// R_max / 128 + E), its y dimension the column tiles.
+template <int G>
+int tile_grouped_launch(const int8_t* aq, const float* as, const int32_t* rmap, int64_t R_max,
+                        int64_t K, const uint8_t* w, const float* ws, int64_t E, int64_t N,
+                        const int32_t* seg_off, const uint16_t* bias, uint16_t* y,
+                        hipStream_t st) {
+    constexpr int BM = 128, BN = 128;
+    const dim3 grid((unsigned)((R_max + BM - 1) / BM + E), (unsigned)((N + BN - 1) / BN));
+    hipLaunchKernelGGL((w4a8_tile_kernel<BM, BN, G, true>), grid, dim3(256), 0, st, aq, K, as,
+                       rmap, (int)R_max, (int)K, w, ws, (int)N, (int)E, seg_off, bias, y, N);
+    return launch_error("w4a8 grouped tile");
 }
 
 template <int G>
@@ -1246,6 +1284,17 @@ int launch_gemm_w4a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, 
         // every step with all eight waves in lockstep, one workgroup per CU, and
         // is 30-45% slower than the 4-wave kernel, which fits two workgroups.
         default: return tile8_launch<256>(xq, ldq, xs, M, K, w, ws, N, bias, y, ldy, st);
+    }
+}
+
+int launch_w4a8_tile_grouped(const int8_t* aq, const float* as, const int32_t* row_index,
+                             int64_t R_max, int64_t K, const uint8_t* w, const float* ws,
+                             int64_t E, int64_t N, int64_t G, const int32_t* seg_off,
+                             const uint16_t* bias, uint16_t* y, hipStream_t st) {
+    switch (G) {
+        case 64: return tile_grouped_launch<64>(aq, as, row_index, R_max, K, w, ws, E, N, seg_off, bias, y, st);
+        case 128: return tile_grouped_launch<128>(aq, as, row_index, R_max, K, w, ws, E, N, seg_off, bias, y, st);
+        default: return tile_grouped_launch<256>(aq, as, row_index, R_max, K, w, ws, E, N, seg_off, bias, y, st);
     }
 }
 

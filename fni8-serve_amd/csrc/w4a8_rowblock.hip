@@ -340,6 +340,11 @@ int launch_gemm_w4a8_grouped(const int8_t* aq, const float* as, const int32_t* r
                              int64_t E, int64_t N, int64_t G, const int32_t* seg_off,
                              const uint16_t* bias, uint16_t* y, hipStream_t st) {
     if (R_max == 0) return FNI8_OK;
+    // 64 or more rows per expert on average: 128x128 segment tiles of the
+    // prefill tile kernel (w4a8.hip)
+    if (R_max >= 64 * E)
+        return launch_w4a8_tile_grouped(aq, as, row_index, R_max, K, w, ws, E, N, G, seg_off,
+                                        bias, y, st);
     switch (G) {
         case 64: return grouped_by_tile<64>(aq, as, row_index, R_max, K, w, ws, E, N, seg_off, bias, y, st);
         case 128: return grouped_by_tile<128>(aq, as, row_index, R_max, K, w, ws, E, N, seg_off, bias, y, st);

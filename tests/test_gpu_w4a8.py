@@ -287,16 +287,17 @@ def test_w4a8_tile8_group256_bitexact(pkg, M, N, K):
 
 
 @pytest.mark.parametrize("T,G,H,I", [(3, 64, 512, 256), (40, 64, 512, 256),
-                                     (200, 128, 1024, 768), (24, 32, 512, 256)])
+                                     (200, 128, 1024, 768), (512, 256, 1024, 768),
+                                     (24, 32, 512, 256)])
 def test_sparse_moe_w4_experts_against_oracle(pkg, T, G, H, I):
     """SparseMoE over per_group_i4 int4 experts (the reference builds experts
     from any QTensor scheme, fni8serve/models/moe.py:56; its converter writes
     per_group_i4 for weight_bits=4, convert.py:130-131): the layer output bit for
     bit against the oracle's sort, per-expert W4A8 chain (gate_up, silu-and-mul,
-    down) and combine, on the same routing.  G = 64 and 128 run the grouped
+    down) and combine, on the same routing.  G = 64..256 run the grouped
     W4A8 GEMM (16-row segment tiles at T = 3 and 40, 64-row ones at T = 200,
-    where down's K = 768 is an odd number of slabs); G = 32 keeps the per-expert
-    modules."""
+    where down's K = 768 is an odd number of slabs, the tile kernel's 128-row
+    ones at T = 512); G = 32 keeps the per-expert modules."""
     print(f"w4 moe T={T} G={G}", flush=True)
     E, k = 16, 4
     experts = [(_w4(pkg, 2 * I, H, G, seed=e), _w4(pkg, H, I, G, seed=100 + e)) for e in range(E)]
@@ -326,11 +327,12 @@ def test_sparse_moe_w4_experts_against_oracle(pkg, T, G, H, I):
 
 @pytest.mark.parametrize("G", [64, 128, 256])
 @pytest.mark.parametrize("K", [768, 1024])
-@pytest.mark.parametrize("per_expert", [1, 20, 60])
+@pytest.mark.parametrize("per_expert", [1, 20, 60, 150])
 def test_w4a8_grouped_gemm_bitexact(pkg, per_expert, K, G):
     """The grouped W4A8 GEMM against the oracle expert by expert: ragged
-    segments (one expert empty), 16-, 32- and 64-row segment tiles (mean rows
-    per expert 1, 20, 60), K = 768 (odd slab count) and 1024, activation rows
+    segments (one expert empty), the row-block kernel's 16-, 32- and 64-row
+    segment tiles (mean rows per expert 1, 20, 60) and the tile kernel's
+    128-row ones (150), K = 768 (odd slab count) and 1024, activation rows
     gathered through a row map, bias, and `rows` beyond the sorted rows (those
     are not written)."""
     print(f"w4a8 grouped per_expert={per_expert} K={K} G={G}", flush=True)
