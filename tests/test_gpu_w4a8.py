@@ -327,16 +327,17 @@ def test_sparse_moe_w4_experts_against_oracle(pkg, T, G, H, I):
 
 @pytest.mark.parametrize("G", [64, 128, 256])
 @pytest.mark.parametrize("K", [768, 1024])
-@pytest.mark.parametrize("per_expert", [1, 20, 60, 150])
-def test_w4a8_grouped_gemm_bitexact(pkg, per_expert, K, G):
+@pytest.mark.parametrize("per_expert,E,N", [(1, 8, 200), (4, 64, 2000), (20, 8, 200),
+                                            (60, 8, 200), (150, 8, 200)])
+def test_w4a8_grouped_gemm_bitexact(pkg, per_expert, E, N, K, G):
     """The grouped W4A8 GEMM against the oracle expert by expert: ragged
-    segments (one expert empty), the row-block kernel's 16-, 32- and 64-row
-    segment tiles (mean rows per expert 1, 20, 60) and the tile kernel's
-    128-row ones (150), K = 768 (odd slab count) and 1024, activation rows
-    gathered through a row map, bias, and `rows` beyond the sorted rows (those
-    are not written)."""
-    print(f"w4a8 grouped per_expert={per_expert} K={K} G={G}", flush=True)
-    E, N = 8, 200
+    segments (one expert empty), the row-block kernel's 16-row segment tiles
+    on two waves (mean 1 row per expert, a small grid) and on four (mean 4, 64
+    experts), its 32- and 64-row tiles (20, 60) and the tile kernel's 128-row
+    ones (150), K = 768 (odd slab count) and 1024, activation rows gathered
+    through a row map, bias, and `rows` beyond the sorted rows (those are not
+    written)."""
+    print(f"w4a8 grouped per_expert={per_expert} E={E} K={K} G={G}", flush=True)
     rng = np.random.default_rng(per_expert + K + G)
     lens = rng.integers(0, 2 * per_expert + 1, E)
     lens[1] = 0
