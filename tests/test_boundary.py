@@ -203,6 +203,44 @@ def test_sparse_moe_w4_experts_cpu_loop(pkg):
     assert torch.equal(y.reshape(5, H), want)
 
 
+def test_sparse_moe_w4_experts_stack_for_the_grouped_kernel(pkg):
+    """int4 experts of one layout (G in 64..256, K a multiple of 256) are stacked
+    for the grouped W4A8 GEMM, with the per-expert modules as views of the
+    stacks; other layouts keep their own modules.  On the CPU both run the
+    reference loop and give the same output as modules built from the original
+    QTensors."""
+    g = torch.Generator().manual_seed(5)
+    E, H, I = 4, 256, 256
+
+    def w4(n, k, G, scale_dtype=torch.float32):
+        codes = torch.randint(-8, 8, (n, k), generator=g)
+        packed = ((codes[:, 0::2] & 0xF) | ((codes[:, 1::2] & 0xF) << 4)).to(torch.uint8)
+        scale = (torch.rand(n, k // G, generator=g) * 0.02 + 1e-3).to(scale_dtype)
+        return pkg.QTensor(packed, scale, scheme="per_group_i4", group_size=G, codebook="int4")
+
+    gate = torch.randn(E, H, generator=g) * 0.05
+    experts = [(w4(2 * I, H, 128), w4(H, I, 64)) for _ in range(E)]
+    moe = pkg.SparseMoE(gate=gate, experts=experts, top_k=2)
+    assert moe.grouped_w4 and not moe.grouped
+    assert moe.w_gate_up.shape == (E, 2 * I, H // 2) and moe.w_gate_up.dtype == torch.uint8
+    assert moe.s_gate_up.shape == (E, 2 * I, H // 128) and moe.s_down.shape == (E, H, I // 64)
+    assert (moe.g_gate_up, moe.g_down) == (128, 64)
+    assert moe.experts[1].gate_up_proj.weight.data.data_ptr() == moe.w_gate_up[1].data_ptr()
+    x = torch.randn(1, 6, H)
+    with torch.inference_mode():
+        y = moe(x)
+        ref = pkg.SparseMoE(gate=gate, experts=experts, top_k=2)
+        ref.experts = torch.nn.ModuleList([pkg.GatedMLP(gu, dn) for gu, dn in experts])
+        want = ref(x)
+    assert torch.equal(y, want)
+    # group size 32, mixed group sizes within a projection, or fp16 scales: not stacked
+    for bad in ([(w4(2 * I, H, 32), w4(H, I, 32)) for _ in range(E)],
+                [(w4(2 * I, H, 128 if e else 64), w4(H, I, 64)) for e in range(E)],
+                [(w4(2 * I, H, 128, torch.float16), w4(H, I, 64)) for _ in range(E)]):
+        m = pkg.SparseMoE(gate=gate, experts=bad, top_k=2)
+        assert not m.grouped_w4 and not m.grouped and len(m.experts) == E
+
+
 def test_sparse_moe_group_limited_routing(pkg):
     """tests/test_deepseek.py:207-265: with 2 groups of 2 experts and topk_group=1,
     every token's experts come from one group."""
