@@ -24,9 +24,11 @@ _F = ctypes.c_float
 
 # name -> argument types; every entry point returns int
 SIGNATURES = {
+    "fni8_init": [],
     "fni8_quantize_rowwise_f16": [_P, _I, _I, _I, _P, _I, _P, _P],
     "fni8_gemm_w8a8": [_P, _I, _P, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P],
     "fni8_linear_w8a8_f16": [_P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P],
+    "fni8_linear_w8a8_f16_ws": [_P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P],
     "fni8_linear_w8a8_f16_noalloc": [_P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P],
     "fni8_moe_sort": [_P, _I, _I, _I, _P, _P, _P, _P],
     "fni8_gemm_w8a8_grouped": [_P, _P, _P, _I, _I, _P, _P, _I, _I, _P, _P, _P, _P, _P],
@@ -41,6 +43,8 @@ SIGNATURES = {
     "fni8_rmsnorm_quant_f16": [_P, _I, _P, _I, _P, _F, _C, _I, _I, _P, _I, _P, _P, _I, _P],
 }
 STRING_FUNCS = ("fni8_strerror", "fni8_last_error", "fni8_version")
+INT64_FUNCS = {"fni8_linear_workspace_bytes": [_I, _I, _I]}
+VOID_FUNCS = {"fni8_debug_coop_wait_ticks": [_I]}
 
 _lib = None
 _lock = threading.Lock()
@@ -69,6 +73,14 @@ def load() -> ctypes.CDLL:
         lib.fni8_last_error.restype = ctypes.c_char_p
         lib.fni8_version.argtypes = []
         lib.fni8_version.restype = ctypes.c_char_p
+        for name, argtypes in VOID_FUNCS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = None
+        for name, argtypes in INT64_FUNCS.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int64
         _lib = lib
         return lib
 
@@ -80,6 +92,11 @@ def call(name: str, *args) -> None:
     if rc != OK:
         msg = f"{name}: {lib.fni8_strerror(rc).decode()}: {lib.fni8_last_error().decode()}"
         raise (ValueError if rc in _ARG_ERRORS else RuntimeError)(msg)
+
+
+def workspace_bytes(M: int, N: int, K: int) -> int:
+    """Workspace bytes fni8_linear_w8a8_f16_ws uses for an [M, K] x [N, K] linear (0: none)."""
+    return int(load().fni8_linear_workspace_bytes(M, N, K))
 
 
 def version() -> str:

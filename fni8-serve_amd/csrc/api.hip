@@ -31,6 +31,8 @@ constexpr int kMaxDevices = 64;
 // write of the same value from two threads is harmless.
 int g_device_ok[kMaxDevices];
 
+int scratch_address(int8_t** out);
+
 int check_device() {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0) {
@@ -44,12 +46,19 @@ int check_device() {
         return FNI8_ERR_DEVICE;
     }
     const bool ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
-    if (dev < kMaxDevices) g_device_ok[dev] = ok ? 1 : -1;
     if (!ok) {
+        if (dev < kMaxDevices) g_device_ok[dev] = -1;
         set_error_detail("device %d is %s; these kernels are built for gfx950", dev,
                          prop.gcnArchName);
         return FNI8_ERR_DEVICE;
     }
+    // The first call on a device also looks up the no-allocation entry point's
+    // scratch address, so that a later call of that entry point under graph
+    // capture makes no runtime query.
+    int8_t* sp = nullptr;
+    const int rc = scratch_address(&sp);
+    if (rc) return rc;
+    if (dev < kMaxDevices) g_device_ok[dev] = 1;
     return FNI8_OK;
 }
 
@@ -146,7 +155,24 @@ int check_rmsnorm(const void* x, int64_t ldx, const void* residual, int64_t ldr,
 
 int linear_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
                   const float* ws, int64_t N, const void* bias, void* y, int64_t ldy, int8_t* xq,
-                  float* xs, int32_t* acc_out, hipStream_t st);
+                  float* xs, int32_t* acc_out, int8_t* work, int64_t work_bytes, hipStream_t st);
+
+int check_linear(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                 const float* ws, int64_t N, const void* bias, const void* y, int64_t ldy,
+                 const int8_t* xq, const float* xs, const int32_t* acc_out) {
+    REQUIRE(x && w && ws && y && xq && xs, FNI8_ERR_NULL,
+            "x, w, ws, y, xq and xs are required");
+    int rc = check_gemm_shape(M, K, N);
+    if (rc) return rc;
+    REQUIRE(ldx >= K && ldy >= N, FNI8_ERR_STRIDE, "ldx=%lld < K or ldy=%lld < N",
+            (long long)ldx, (long long)ldy);
+    REQUIRE(aligned(x, 2) && aligned(xq, 4) && aligned(w, 4), FNI8_ERR_ALIGN,
+            "x, xq or w misaligned");
+    REQUIRE(aligned(xs, 4) && aligned(ws, 4) && aligned(y, 2) && aligned(bias, 2) &&
+                aligned(acc_out, 4),
+            FNI8_ERR_ALIGN, "scale/output pointers misaligned");
+    return FNI8_OK;
+}
 
 }  // namespace
 
@@ -168,6 +194,32 @@ const char* fni8_strerror(int code) {
 const char* fni8_last_error(void) { return fni8h::g_detail; }
 
 const char* fni8_version(void) { return "fni8amd 0.1.0 gfx950"; }
+
+int fni8_init(void) {
+    fni8h::g_detail[0] = 0;
+    int count = 0, cur = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) {
+        set_error_detail("no HIP device");
+        return FNI8_ERR_DEVICE;
+    }
+    if (hipGetDevice(&cur) != hipSuccess) cur = 0;
+    int rc = FNI8_OK;
+    for (int d = 0; d < count && d < kMaxDevices; d++) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, d) != hipSuccess ||
+            strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+            continue;  // other devices are left alone
+        if (hipSetDevice(d) != hipSuccess) {
+            set_error_detail("hipSetDevice(%d) failed", d);
+            rc = FNI8_ERR_DEVICE;
+            break;
+        }
+        rc = check_device();
+        if (rc) break;
+    }
+    (void)hipSetDevice(cur);
+    return rc;
+}
 
 int fni8_quantize_rowwise_f16(const void* x, int64_t M, int64_t K, int64_t ldx, int8_t* xq,
                               int64_t ldq, float* xs, void* stream) {
@@ -210,22 +262,35 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
                          const float* ws, int64_t N, const void* bias, void* y, int64_t ldy,
                          int8_t* xq, float* xs, int32_t* acc_out, void* stream) {
     fni8h::g_detail[0] = 0;
-    REQUIRE(x && w && ws && y && xq && xs, FNI8_ERR_NULL,
-            "x, w, ws, y, xq and xs are required");
-    int rc = check_gemm_shape(M, K, N);
+    int rc = check_linear(x, ldx, M, K, w, ws, N, bias, y, ldy, xq, xs, acc_out);
     if (rc) return rc;
-    REQUIRE(ldx >= K && ldy >= N, FNI8_ERR_STRIDE, "ldx=%lld < K or ldy=%lld < N",
-            (long long)ldx, (long long)ldy);
-    REQUIRE(aligned(x, 2) && aligned(xq, 4) && aligned(w, 4), FNI8_ERR_ALIGN,
-            "x, xq or w misaligned");
-    REQUIRE(aligned(xs, 4) && aligned(ws, 4) && aligned(y, 2) && aligned(bias, 2) &&
-                aligned(acc_out, 4),
-            FNI8_ERR_ALIGN, "scale/output pointers misaligned");
+    rc = check_device();
+    if (rc) return rc;
+    return linear_launch(x, ldx, M, K, w, ws, N, bias, y, ldy, xq, xs, acc_out, nullptr, 0,
+                         (hipStream_t)stream);
+}
+
+int fni8_linear_w8a8_f16_ws(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                            const float* ws, int64_t N, const void* bias, void* y, int64_t ldy,
+                            int8_t* xq, float* xs, int32_t* acc_out, void* workspace,
+                            int64_t workspace_bytes, void* stream) {
+    fni8h::g_detail[0] = 0;
+    int rc = check_linear(x, ldx, M, K, w, ws, N, bias, y, ldy, xq, xs, acc_out);
+    if (rc) return rc;
+    REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 256)), FNI8_ERR_ALIGN,
+            "workspace must be 256-byte aligned with a size >= 0");
     rc = check_device();
     if (rc) return rc;
     return linear_launch(x, ldx, M, K, w, ws, N, bias, y, ldy, xq, xs, acc_out,
+                         static_cast<int8_t*>(workspace), workspace ? workspace_bytes : 0,
                          (hipStream_t)stream);
 }
+
+int64_t fni8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    return fni8h::coop_workspace_bytes(M, N, K);
+}
+
+void fni8_debug_coop_wait_ticks(int64_t ticks) { fni8h::set_coop_wait_ticks(ticks); }
 
 int fni8_linear_w8a8_f16_noalloc(const void* x, int64_t ldx, int64_t M, int64_t K,
                                  const int8_t* w, const float* ws, int64_t N, const void* bias,
@@ -246,12 +311,15 @@ int fni8_linear_w8a8_f16_noalloc(const void* x, int64_t ldx, int64_t M, int64_t 
     int8_t* sp = nullptr;
     rc = scratch_address(&sp);
     if (rc) return rc;
-    // xq: M rows of K bytes at the start; xs: M floats after the xq area.  Every
-    // byte the GEMM reads is written by this call's quantization first, so nothing
-    // needs clearing between calls.
+    // xq: M rows of K bytes at the start; xs: M floats after the xq area; the
+    // rest of the xq area (past M * K, 256-aligned) is the one-launch path's
+    // workspace.  Every byte the GEMM reads is written by this call's
+    // quantization first, and the workspace needs no clearing, so nothing is
+    // cleared between calls.
+    const int64_t work_off = (M * K + 255) & ~(int64_t)255;
     return linear_launch(x, ldx, M, K, w, ws, N, bias, y, ldy, sp,
-                         reinterpret_cast<float*>(sp + kNoAllocQBytes), nullptr,
-                         (hipStream_t)stream);
+                         reinterpret_cast<float*>(sp + kNoAllocQBytes), nullptr, sp + work_off,
+                         kNoAllocQBytes - work_off, (hipStream_t)stream);
 }
 
 }  // extern "C"
@@ -261,8 +329,15 @@ namespace {
 // The launches of the whole W8A8 linear on caller-checked arguments.
 int linear_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
                   const float* ws, int64_t N, const void* bias, void* y, int64_t ldy, int8_t* xq,
-                  float* xs, int32_t* acc_out, hipStream_t st) {
+                  float* xs, int32_t* acc_out, int8_t* work, int64_t work_bytes, hipStream_t st) {
     int rc;
+    // 5..16 tokens with a workspace: one launch, the quantization shared per XCD
+    if (M >= 5 && work != nullptr) {
+        rc = fni8h::launch_decode_coop((const uint16_t*)x, ldx, M, K, w, ws, N,
+                                       (const uint16_t*)bias, (uint16_t*)y, ldy, xq, xs, acc_out,
+                                       work, work_bytes, st);
+        if (rc != 1) return rc;
+    }
     // Decode sizes: one launch, the quantization fused into the GEMM -- on MFMA
     // for 3..4 tokens, as a dot4 GEMV for 1..2 (and shapes the MFMA kernel does
     // not take), where the streaming loop without an LDS pass is faster.

@@ -401,6 +401,14 @@ int launch_decode_mfma_grouped(const int8_t* aq, int64_t lda, const float* as,
                                const int8_t* w, const float* ws, int64_t E, int64_t N,
                                const int32_t* seg_off, const uint16_t* bias, uint16_t* y,
                                int64_t ldy, int32_t* acc_out, hipStream_t st);
+// Decode linear for 5 <= M <= 16 in one launch, the quantization shared per XCD
+// through `work`; returns 1 when not taken (the caller then uses two launches).
+int64_t coop_workspace_bytes(int64_t M, int64_t N, int64_t K);
+void set_coop_wait_ticks(int64_t ticks);
+int launch_decode_coop(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                       const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
+                       int64_t ldy, int8_t* xq_out, float* xs_out, int32_t* acc_out,
+                       int8_t* work, int64_t work_bytes, hipStream_t st);
 // Decode GEMM (M <= 64, pre-quantized activations) on MFMA; returns 1 when not taken.
 int launch_decode_mfma(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
                        const int8_t* w, const float* ws, int64_t N, const uint16_t* bias,

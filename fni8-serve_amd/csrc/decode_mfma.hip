@@ -33,99 +33,16 @@
 // flight.  Each workgroup quantizes the rows for itself (no workgroup waits
 // for another); on MFMA the dot products cost no VALU time, which is what made
 // the dot4 GEMV slow at M = 4.
-#include "common.h"
+#include "decode_tile.h"
 
 namespace {
 
-__device__ __forceinline__ i32x4 ld16(const void* p) {
-    return *reinterpret_cast<const i32x4*>(p);
-}
-__device__ __forceinline__ i32x4 ld16_nt(const int8_t* p) {
-    return __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(p));
-}
-
-// 16-byte chunk position of (row, chunk) inside a 128-byte row of an LDS tile:
-// rows r and r' with r = r' mod 4 get different chunk positions, so the 16
-// lanes of one ds_read_b128 pass (16 rows, one chunk) hit 16 distinct slots.
-__device__ __forceinline__ int swz(int row, int chunk) {
-    return ((chunk ^ (row & 7) ^ ((row >> 3) & 7)) & 7) * 16;
-}
-
-// Barrier that waits for LDS traffic only: the compiler's __syncthreads also
-// waits for every outstanding global load, which would drain the weight
-// prefetch.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// Weight side of one wave: pointers and LDS offsets for the 2*NB load
-// instructions of a slab, and the B-fragment offsets for the MFMA.
-// RB = 8-row load groups of the workgroup (at most 2 * NB): a workgroup may own
-// fewer rows than its NB MFMA blocks span, so that the workgroup count fits the
-// CUs (6144 rows in 24-row workgroups are 256 of them); the MFMA reads the
-// unloaded rows of the tile as whatever they hold, and those columns are never
-// stored.
-template <int NB, int RB = 2 * NB>
-struct WeightLanes {
-    static_assert(RB >= 1 && RB <= 2 * NB, "load groups within the MFMA blocks");
-    const int8_t* src[RB];
-    int woff[RB];
-    int roff[NB][2];
-    __device__ __forceinline__ void init(const int8_t* w, int n0, int N, int64_t K, int s0,
-                                         int lane) {
-        const int rq = lane >> 3, c = lane & 7, r = lane & 15, g = lane >> 4;
-#pragma unroll
-        for (int h = 0; h < RB; h++) {
-            const int row = h * 8 + rq;
-            int n = n0 + row;
-            n = n < N ? n : N - 1;  // rows past N load real memory, never stored
-            src[h] = w + (int64_t)n * K + (int64_t)s0 * 128 + c * 16;
-            woff[h] = row * 128 + swz(row, c);
-        }
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-#pragma unroll
-            for (int q = 0; q < 2; q++) roff[b][q] = (b * 16 + r) * 128 + swz(b * 16 + r, 4 * q + g);
-    }
-};
-
-// Cross-wave reduction and epilogue shared by both kernels.  acc[q][mt][b]:
-// lane l, register i holds token mt*16 + 4*(l/16) + i, row b*16 + l%16.
-// Token m of the tile is output row r0 + m; its activation scale is
-// xs[rmap[r0 + m]] (xs[r0 + m] without a row map).
-template <int MT, int NB, int WAVES, int WROWS = 16 * NB>
-__device__ __forceinline__ void reduce_store(i32x4 (&acc)[2][MT][NB], i32x4* red, int wave,
-                                             int lane, int tid, int n0, int r0, int M, int N,
-                                             const float* xs, const int32_t* __restrict__ rmap,
-                                             const float* __restrict__ ws,
-                                             const uint16_t* __restrict__ bias,
-                                             uint16_t* __restrict__ y, int64_t ldy,
-                                             int32_t* __restrict__ acc_out) {
-#pragma unroll
-    for (int mt = 0; mt < MT; mt++)
-#pragma unroll
-        for (int b = 0; b < NB; b++)
-            red[(wave * MT * NB + mt * NB + b) * 64 + lane] = acc[0][mt][b] + acc[1][mt][b];
-    __syncthreads();
-    for (int idx = tid; idx < MT * NB * 64; idx += WAVES * 64) {
-        const int mb = idx >> 6, ln = idx & 63, mt = mb / NB, b = mb % NB;
-        i32x4 s = red[mb * 64 + ln];
-#pragma unroll
-        for (int wv = 1; wv < WAVES; wv++) s += red[(wv * MT * NB + mb) * 64 + ln];
-        const int col = n0 + b * 16 + (ln & 15);
-        if (b * 16 + (ln & 15) >= WROWS || col >= N) continue;
-        const float wsc = ws[col];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int m = mt * 16 + (ln >> 4) * 4 + i;
-            if (m >= M) continue;
-            const int row = r0 + m;
-            const float xsc = xs[rmap != nullptr ? rmap[row] : row];
-            y[(int64_t)row * ldy + col] = fni8::dequant_one(s[i], xsc, wsc, bias, col);
-            if (acc_out != nullptr) acc_out[(int64_t)row * N + col] = s[i];
-        }
-    }
-}
+using fni8dec::ld16;
+using fni8dec::ld16_nt;
+using fni8dec::lds_barrier;
+using fni8dec::reduce_store;
+using fni8dec::swz;
+using fni8dec::WeightLanes;
 
 // ---- int8 activations, M <= 16*MT ------------------------------------------
 // GROUPED: the expert-segment form of the MoE layer (segments seg_off[E+1] of

@@ -1,6 +1,6 @@
 // W4A8 decode GEMM on MFMA with the weight rows split over the waves (gemm_w4a8
 // of `fni8.linear` for int4 QTensors, fni8serve/layers/linear.py:9, :63-65),
-// for 5 to 64 tokens of int8 activations.
+// for 9 to 64 tokens of int8 activations on wide weights (N >= 16384).
 //
 // w4a8_mfma_kernel (w4a8.hip) splits K over the waves of a 16-row workgroup and
 // moves every group's int32 sums through LDS to fold them in order; each

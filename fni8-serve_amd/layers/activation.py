@@ -2,12 +2,14 @@
 
 SiluAndMul (Qwen3) and GeluAndMul (Gemma, tanh form) split [..., 2I] into gate
 and up and return act(gate) * up.  As in the reference (`_fused_ok`,
-activation.py:16-17, :24, :40), a GPU tensor takes the fused kernel
-(`ops.act_and_mul`, one launch); CPU tensors and the exact-erf gelu take the
-eager torch form.  The kernel needs fp16 on the GPU: other GPU dtypes raise
-rather than fall back.  `fused_act(module)` names the kernel activation a
-module computes, so GatedMLP and SparseMoE can fuse it with the down
-projection's quantization.
+activation.py:16-17, :24, :40), a GPU fp16 tensor takes the fused kernel
+(`ops.act_and_mul`, one launch).  Every other input takes the eager torch form
+`act(gate) * up` in the input's own dtype: CPU tensors, the exact-erf gelu,
+GPU fp32 (which the reference also computes eagerly) and GPU bf16 (which the
+reference sends to its closed fused kernel; the kernel here is fp16-only, and
+the bf16 result is torch's).  No input raises where the reference returns a
+result.  `fused_act(module)` names the kernel activation a module computes, so
+GatedMLP and SparseMoE can fuse it with the down projection's quantization.
 """
 from __future__ import annotations
 
@@ -19,11 +21,7 @@ from .. import ops
 
 
 def _kernel_ok(x: torch.Tensor) -> bool:
-    if not x.is_cuda:
-        return False
-    if x.dtype != torch.float16:
-        raise ValueError(f"act_and_mul on the GPU expects fp16 (got {x.dtype})")
-    return True
+    return x.is_cuda and x.dtype == torch.float16
 
 
 class SiluAndMul(nn.Module):

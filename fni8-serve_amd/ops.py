@@ -142,9 +142,17 @@ def linear_with_intermediates(x: torch.Tensor, qt: QTensor, bias: torch.Tensor |
     acc = torch.empty((M, N), dtype=torch.int32, device=dev) if want_acc else None
     if M == 0:
         return y, xq, xs, acc
+    # 5..16 tokens on the narrower weights: the one-launch path exchanges the
+    # quantized rows through a workspace.  It comes from the caching allocator like every other buffer:
+    # torch hands a block back to the same stream only, after the work queued
+    # on it, so no two calls that can overlap share one; its contents never
+    # matter, so it is not cleared.
+    nw = _lib.workspace_bytes(M, N, K)
+    work = torch.empty(nw, dtype=torch.uint8, device=dev) if nw else None
     with torch.cuda.device(dev):
-        _lib.call("fni8_linear_w8a8_f16", _ptr(x2), ldx, M, K, _ptr(w), _ptr(ws), N,
-                  _ptr(bias), _ptr(y), N, _ptr(xq), _ptr(xs), _ptr(acc), _stream(dev))
+        _lib.call("fni8_linear_w8a8_f16_ws", _ptr(x2), ldx, M, K, _ptr(w), _ptr(ws), N,
+                  _ptr(bias), _ptr(y), N, _ptr(xq), _ptr(xs), _ptr(acc), _ptr(work), nw,
+                  _stream(dev))
     return y, xq, xs, acc
 
 

@@ -11,9 +11,10 @@
  *   - Pointers are device pointers on the current HIP device; `stream` is a
  *     hipStream_t (NULL = the legacy default stream).  Work is enqueued on
  *     `stream`; nothing synchronises the host.
- *   - The library allocates no device memory and holds no mutable global
- *     state; every buffer comes from the caller, so calls can be captured in
- *     a HIP graph.  Calls are reentrant.
+ *   - The library allocates no device memory; every buffer comes from the
+ *     caller, so calls can be captured in a HIP graph.  Calls are reentrant.
+ *     The one piece of mutable global state is the per-GPU scratch of
+ *     fni8_linear_w8a8_f16_noalloc (below), which only that entry point uses.
  *   - fp16 tensors are IEEE binary16 passed as `void*` / `uint16_t*`.
  *   - Weights follow the per_row_i8 QTensor layout (models/weights.py:18-25):
  *     data int8 [N, K] row-major (K contiguous), scale fp32 [N].
@@ -52,6 +53,16 @@ const char* fni8_last_error(void);
 
 /* Library version string. */
 const char* fni8_version(void);
+
+/*
+ * Optional set-up, no counterpart in the reference: checks every visible
+ * gfx950 device and looks up, with that device current, the address of the
+ * per-GPU scratch that fni8_linear_w8a8_f16_noalloc uses.  Every entry point
+ * does the same for the current device on its first call there, so only a
+ * caller whose first call on a device may happen under HIP graph capture needs
+ * it (call it before capturing).  Restores the current device.
+ */
+int fni8_init(void);
 
 /*
  * Per-token symmetric activation quantization: step 1 of `fni8.linear`
@@ -94,6 +105,46 @@ int fni8_gemm_w8a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, in
 int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
                          const float* ws, int64_t N, const void* bias, void* y, int64_t ldy,
                          int8_t* xq, float* xs, int32_t* acc_out, void* stream);
+
+/*
+ * fni8_linear_w8a8_f16 with a workspace: the same call, arithmetic and
+ * outputs (bit for bit), in one launch instead of two where that measured
+ * faster -- 5 <= M <= 16 tokens on QKV- and down-shaped weights, 5 <= M <= 8
+ * on O-shaped ones
+ * (replaces fni8serve/layers/linear.py:69 at decode batch sizes).  The
+ * per-token quantization then runs once per XCD and reaches the GEMM
+ * workgroups through that XCD's L2; `workspace` holds the exchanged rows.
+ * Other shapes take the same launches as fni8_linear_w8a8_f16.
+ *   workspace        device memory, 256-byte aligned, at least
+ *                    fni8_linear_workspace_bytes(M, N, K) bytes; any contents
+ *                    (nothing needs clearing, before the first call or
+ *                    between calls); NULL or too small = the two-launch path
+ *   Two calls that may run at the same time must not share a workspace (one
+ *   workspace per stream), as they must not share xq / xs.
+ */
+int fni8_linear_w8a8_f16_ws(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
+                            const float* ws, int64_t N, const void* bias, void* y, int64_t ldy,
+                            int8_t* xq, float* xs, int32_t* acc_out, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes fni8_linear_w8a8_f16_ws uses for M tokens, N outputs and K
+ * inputs: 8 * (2304 + M * K rounded up to 256) where the one-launch path takes
+ * the shape (5 <= M <= 16 with 4096 < N < 16384 and K = 4096, or N <= 4096 and
+ * K = 12288; 5 <= M <= 8 with N <= 4096 and K = 4096), else 0 (no workspace is
+ * used).  At most 8 * (2304 + 16 * 12288) = 1,591,296.
+ */
+int64_t fni8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
+/*
+ * Test hook, no counterpart in the reference: the bound, in ticks of the
+ * 100 MHz real-time counter, on how long a GEMM workgroup of the one-launch
+ * path waits for its XCD's quantized rows before quantizing them itself
+ * (default 10000 = 100 us; a negative value restores it).  0 makes every
+ * workgroup that does not find the rows at its first look take the fallback,
+ * which must give the same bits.  Process-wide; affects later launches.
+ */
+void fni8_debug_coop_wait_ticks(int64_t ticks);
 
 /*
  * fni8_linear_w8a8_f16 for callers that cannot allocate (code under HIP graph

@@ -12,7 +12,8 @@ HEADER = os.path.join(ROOT, "include", "fni8amd.h")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(fni8_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|void|const char\*)\s+(fni8_\w+)\s*\(",
+                                 text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -36,9 +37,9 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_binding_covers_every_declared_compute_entry(pkg):
     from importlib import import_module
-    sigs = import_module("fni8serve_amd._lib").SIGNATURES
-    strings = import_module("fni8serve_amd._lib").STRING_FUNCS
-    assert set(_declared()) == set(sigs) | set(strings)
+    b = import_module("fni8serve_amd._lib")
+    assert set(_declared()) == (set(b.SIGNATURES) | set(b.STRING_FUNCS) | set(b.INT64_FUNCS)
+                                | set(b.VOID_FUNCS))
 
 
 def test_version_and_error_strings(lib):
@@ -137,3 +138,30 @@ def test_moe_route_argument_errors(lib):
                               None) == -2
     assert lib.fni8_moe_route(fake, 2, 128, 100, 0, None, 0, 0, 8, 1, F(1.0), fake, fake, None) == -4
     assert lib.fni8_moe_route(fake, 1, 128, 128, 0, None, 0, 0, 8, 1, F(1.0), None, fake, None) == -1
+
+
+def test_workspace_size_and_argument_checks(lib):
+    """The one-launch path's workspace: 8 regions of (2304 + M*K rounded up to
+    256) bytes for the shapes it takes (5 <= M <= 16; QKV-, O- and down-shaped
+    weights), none otherwise; a misaligned workspace is an argument error
+    raised before any launch."""
+    for M, N, K in ((5, 4096, 4096), (8, 4096, 4096), (16, 6144, 4096), (7, 4096, 12288),
+                    (8, 100, 4096), (16, 4096, 12288)):
+        assert lib.fni8_linear_workspace_bytes(M, N, K) == 8 * (2304 + ((M * K + 255) // 256) * 256)
+    assert lib.fni8_linear_workspace_bytes(16, 4096, 12288) == 1591296
+    for M, N, K in ((0, 4096, 4096), (1, 4096, 4096), (4, 4096, 4096), (9, 4096, 4096),
+                    (17, 6144, 4096),
+                    (64, 4096, 4096), (16, 24576, 4096), (16, 6144, 12288), (16, 4096, 1024),
+                    (16, 4096, 8192)):
+        assert lib.fni8_linear_workspace_bytes(M, N, K) == 0, (M, N, K)
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    rc = lib.fni8_linear_w8a8_f16_ws(fake, 4096, 16, 4096, fake, fake, 64, None, fake, 64, fake,
+                                     fake, None, P(0x1080), 1 << 20, None)
+    assert rc == -3 and b"workspace" in lib.fni8_last_error()
+    rc = lib.fni8_linear_w8a8_f16_ws(None, 4096, 16, 4096, fake, fake, 64, None, fake, 64, fake,
+                                     fake, None, fake, 1 << 20, None)
+    assert rc == -1
+    rc = lib.fni8_linear_w8a8_f16_ws(fake, 4096, 16, 4096, fake, fake, 64, None, fake, 64, fake,
+                                     fake, None, fake, -1, None)
+    assert rc == -3

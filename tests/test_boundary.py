@@ -159,6 +159,20 @@ def test_rmsnorm_cpu_is_the_reference_eager_form(pkg):
         pkg.act_and_mul(torch.randn(2, 8).half())
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+def test_act_and_mul_modules_on_the_cpu_are_the_eager_form(pkg, dt):
+    """CPU tensors of every dtype take act(gate) * up in their own dtype
+    (fni8serve/layers/activation.py:26-27, :42-43); only GPU fp16 takes the kernel."""
+    import torch.nn.functional as F
+    from fni8serve_amd.layers import activation as act
+    x = (torch.randn(3, 64, generator=torch.Generator().manual_seed(5)) * 2).to(dt)
+    gate, up = x.chunk(2, dim=-1)
+    assert torch.equal(act.SiluAndMul()(x), F.silu(gate) * up)
+    assert torch.equal(act.GeluAndMul("tanh")(x), F.gelu(gate, approximate="tanh") * up)
+    assert torch.equal(act.GeluAndMul("none")(x), F.gelu(gate) * up)
+    assert not act._kernel_ok(x)
+
+
 def _moe(pkg, E=4, H=64, I=32, k=2, **kw):
     g = torch.Generator().manual_seed(0)
     experts = [(pkg.to_qtensor(torch.randn(2 * I, H, generator=g) * 0.05),

@@ -195,6 +195,28 @@ def test_rmsnorm_module_other_dtypes_take_eager_form(pkg, dt):
     assert torch.equal(h.cpu(), x + r)
 
 
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("mod", ["silu", "gelu_pytorch_tanh", "gelu"])
+def test_act_and_mul_module_other_dtypes_take_eager_form(pkg, dt, mod):
+    """GPU inputs the fp16 kernel does not take (fp32, bf16) return the eager
+    act(gate) * up in their own dtype instead of raising; the reference computes
+    fp32 the same way (fni8serve/layers/activation.py:16-17, :26-27, :42-43)."""
+    print(f"act_and_mul module {mod} {dt}", flush=True)
+    from fni8serve_amd.layers import activation as act
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(22)
+    x = (torch.randn(6, 2 * 384, generator=g) * 3).to(dt)
+    m = act.get_act_and_mul(mod)
+    got = m(x.cuda())
+    torch.cuda.synchronize()
+    gate, up = x.float().chunk(2, dim=-1)
+    appr = getattr(m, "approximate", None)
+    ref = (F.silu(gate) if appr is None else F.gelu(gate, approximate=appr)) * up
+    assert got.dtype == dt and got.shape == (6, 384)
+    tol = 1e-5 if dt == torch.float32 else 2e-2
+    assert torch.allclose(got.cpu().float(), ref, rtol=tol, atol=tol)
+
+
 def test_rmsnorm_against_torch_fp32(pkg):
     """Against the reference's eager form evaluated by torch on the GPU in fp32
     (norm.py:37-43): within 1 fp16 ulp; max abs / rel error printed."""

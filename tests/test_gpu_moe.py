@@ -284,3 +284,46 @@ def test_combine_skips_out_of_range_experts(pkg, cuda, k):
     out_r = oracle.moe_combine_f16(y, topi, np.where(bad, np.float16(0), topw),
                                    np.where(bad, 0, pos_h).astype(np.int32))
     assert np.array_equal(out.cpu().numpy().view(np.uint16), out_r.view(np.uint16))
+
+
+@pytest.mark.parametrize("T", [16, 256])
+def test_sparse_moe_int8_layer_against_oracle_qwen3_30b_shape(pkg, wl, cuda, T):
+    """The whole SparseMoE layer over per_row_i8 experts at the Qwen3-30B-A3B
+    expert shape (128 experts, top-8, hidden 2048, intermediate 768), bit for
+    bit against the oracle's restatement of the reference's expert loop
+    (fni8serve/models/moe.py:97-105) on the module's own routing: the stable
+    sort, per expert linear_w8a8_f16 (gate_up) -> act_and_mul_f16 (silu) ->
+    linear_w8a8_f16 (down), and the fp16 index_add combine in expert order."""
+    print(f"int8 moe layer T={T}", flush=True)
+    E, k, H, I = wl.MOE["experts"], wl.MOE["top_k"], 2048, 768
+    g = torch.Generator().manual_seed(T)
+
+    def qt(n, kk, seed):
+        q, _ = wl.weight_i8(n, kk, seed=seed)
+        s = (torch.rand(n, generator=g) * 0.0015 + 0.0005).float()
+        return pkg.QTensor(q.cuda(), s.cuda(), scheme="per_row_i8")
+    experts = [(qt(2 * I, H, 2000 + e), qt(H, I, 3000 + e)) for e in range(E)]
+    gate = (torch.randn(E, H, generator=g) * 0.05).half().cuda()
+    moe = pkg.SparseMoE(gate=gate, experts=experts, top_k=k, norm_topk_prob=True)
+    x = (wl.activations(T, H, seed=T + 11) * 0.5).cuda().reshape(1, T, H)
+    with torch.inference_mode():
+        out = moe(x)
+        topw, topi = moe.route(x.reshape(-1, H))
+    torch.cuda.synchronize()
+    seg, rt, _, pos = oracle.moe_sort(topi.cpu().numpy(), E)
+    xf = x.reshape(-1, H).cpu().numpy()
+    ys = np.zeros((T * k, H), np.float16)
+    for e in range(E):
+        lo, hi = int(seg[e]), int(seg[e + 1])
+        if hi == lo:
+            continue
+        gu, dn = experts[e]
+        h, _, _, _ = oracle.linear_w8a8_f16(xf[rt[lo:hi]], gu.data.cpu().numpy(),
+                                            gu.scale.cpu().numpy(), None)
+        a = oracle.act_and_mul_f16(h, "silu")
+        yd, _, _, _ = oracle.linear_w8a8_f16(a, dn.data.cpu().numpy(), dn.scale.cpu().numpy(), None)
+        ys[lo:hi] = yd
+    want = oracle.moe_combine_f16(ys, topi.cpu().numpy(), topw.cpu().numpy(), pos)
+    got = out.reshape(T, H).cpu().numpy()
+    assert np.isfinite(want.astype(np.float32)).all()
+    assert np.array_equal(got.view(np.uint16), want.view(np.uint16))

@@ -79,6 +79,31 @@ def test_w4a8_qwen3_8b_shapes_sampled(pkg, M, shape):
     _check(pkg, _x(M, K, seed=M), qt, None, rows, cols)
 
 
+@pytest.mark.parametrize("G", [32, 64, 128, 256])
+@pytest.mark.parametrize("shape", [(4096, 4096), (3072, 2048), (4096, 12288)],
+                         ids=["o", "n3072_k2048", "down"])
+def test_w4a8_one_token_launch_table_bitexact(pkg, shape, G):
+    """One token at the launch table's stream shapes (O-like K <= 4096, N <= 4096
+    with 8 | K/256, and the down shape): the fused launch (fp16 x) and the
+    prequantized GEMM, with bias, against the oracle on the first and last 64
+    columns and 128 sampled ones (each output column depends only on its own
+    weight row)."""
+    print(f"w4a8 one-token table shape={shape} G={G}", flush=True)
+    N, K = shape
+    qt = _w4(pkg, N, K, G, seed=N + K + G)
+    bias = torch.randn(N, device="cuda").half()
+    rng = np.random.default_rng(N + G)
+    cols = np.unique(np.concatenate([np.arange(64), np.arange(N - 64, N),
+                                     rng.choice(N, 128, replace=False)]))
+    x = _x(1, K, seed=K + G)
+    _check(pkg, x, qt, bias, None, cols)
+    xq, xs = pkg.quantize_rowwise(x)
+    y = pkg.gemm_w4a8(xq, xs, qt, bias)
+    want = o.gemm_w4a8(xq.cpu().numpy(), xs.cpu().numpy(), qt.data.cpu().numpy()[cols],
+                       qt.scale.cpu().numpy()[cols], G, bias=bias.cpu().numpy()[cols])
+    assert np.array_equal(y.cpu().numpy()[:, cols].view(np.uint16), want.view(np.uint16))
+
+
 def test_w4a8_matches_the_reference_seam_test(pkg):
     """tests/test_smoke.py:83-94: W4A8 against F.linear with the fp16
     dequantized weight, cosine >= 0.985 in the reference; printed here."""
@@ -322,6 +347,46 @@ def test_sparse_moe_w4_experts_against_oracle(pkg, T, G, H, I):
         yd, _, _ = o.linear_w4a8_f16(a, dn.data.cpu().numpy(), dn.scale.cpu().numpy(), G)
         ys[lo:hi] = yd
     want = o.moe_combine_f16(ys, topi.cpu().numpy(), topw.cpu().numpy(), pos)
+    assert np.array_equal(out.reshape(T, H).cpu().numpy().view(np.uint16), want.view(np.uint16))
+
+
+@pytest.mark.parametrize("T", [16, 256])
+def test_sparse_moe_w4_layer_qwen3_30b_shape(pkg, T):
+    """The int4-expert SparseMoE layer at the Qwen3-30B-A3B expert shape the
+    benchmark times (128 experts, top-8, hidden 2048, intermediate 768, group
+    128) on the grouped W4A8 GEMM, bit for bit against the oracle chain: sort,
+    per expert linear_w4a8_f16 (gate_up) -> silu-and-mul -> linear_w4a8_f16
+    (down), combine (fni8serve/models/moe.py:97-105)."""
+    print(f"w4 moe layer qwen3-30b T={T}", flush=True)
+    E, k, H, I, G = 128, 8, 2048, 768, 128
+    experts = [(_w4(pkg, 2 * I, H, G, seed=4000 + e), _w4(pkg, H, I, G, seed=5000 + e))
+               for e in range(E)]
+    for gu, dn in experts:  # smaller scales keep every fp16 partial finite
+        gu.scale.mul_(0.1)
+        dn.scale.mul_(0.1)
+    g = torch.Generator(device="cuda").manual_seed(T)
+    gate = (torch.randn(E, H, device="cuda", generator=g) * 0.05).half()
+    moe = pkg.SparseMoE(gate=gate, experts=experts, top_k=k, norm_topk_prob=True)
+    assert moe.grouped_w4
+    x = (_x(T, H, seed=T + 17) * 0.5).reshape(1, T, H)
+    with torch.inference_mode():
+        out = moe(x)
+        topw, topi = moe.route(x.reshape(-1, H))
+    torch.cuda.synchronize()
+    seg, rt, _, pos = o.moe_sort(topi.cpu().numpy(), E)
+    xf = x.reshape(-1, H).cpu().numpy()
+    ys = np.zeros((T * k, H), np.float16)
+    for e in range(E):
+        lo, hi = int(seg[e]), int(seg[e + 1])
+        if hi == lo:
+            continue
+        gu, dn = experts[e]
+        h, _, _ = o.linear_w4a8_f16(xf[rt[lo:hi]], gu.data.cpu().numpy(), gu.scale.cpu().numpy(), G)
+        a = o.act_and_mul_f16(h, "silu")
+        yd, _, _ = o.linear_w4a8_f16(a, dn.data.cpu().numpy(), dn.scale.cpu().numpy(), G)
+        ys[lo:hi] = yd
+    want = o.moe_combine_f16(ys, topi.cpu().numpy(), topw.cpu().numpy(), pos)
+    assert np.isfinite(want.astype(np.float32)).all()
     assert np.array_equal(out.reshape(T, H).cpu().numpy().view(np.uint16), want.view(np.uint16))
 
 
