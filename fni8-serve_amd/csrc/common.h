@@ -405,6 +405,9 @@ int launch_decode_mfma_grouped(const int8_t* aq, int64_t lda, const float* as,
 // through `work`; returns 1 when not taken (the caller then uses two launches).
 int64_t coop_workspace_bytes(int64_t M, int64_t N, int64_t K);
 void set_coop_wait_ticks(int64_t ticks);
+// The bound (100 MHz real-time ticks) on a GEMM workgroup's wait for the rows
+// its XCD's producers publish.
+uint64_t xcd_wait_ticks();
 int launch_decode_coop(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
                        const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
                        int64_t ldy, int8_t* xq_out, float* xs_out, int32_t* acc_out,

@@ -51,16 +51,18 @@
 // so the launch table takes QKV and down up to 16 tokens and O up to 8.
 #include "decode_tile.h"
 
-extern "C" __device__ uint64_t fni8_llvm_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
-
 namespace {
 
+using fni8dec::dispatch_tag;
 using fni8dec::ld16;
 using fni8dec::ld16_nt;
 using fni8dec::lds_barrier;
+using fni8dec::poll_flag;
+using fni8dec::publish_flag;
 using fni8dec::reduce_store;
 using fni8dec::swz;
 using fni8dec::WeightLanes;
+using fni8dec::xcc_id;
 
 // Workspace: one region per XCD -- flags [16] u64, one per 128-byte line (the
 // polls of one XCD's workgroups then spread over the L2 channels instead of
@@ -76,27 +78,6 @@ constexpr int kFallbackRows = 4;  // rows a GEMM workgroup quantizes per pass on
 // hook (fni8_debug_coop_wait_ticks) can lower it to force the fallback.
 constexpr int64_t kWaitTicks = 10000;
 int64_t g_wait_ticks = kWaitTicks;
-
-__device__ __forceinline__ uint32_t xcc_id() {
-    uint32_t v;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-    return v & (kXcds - 1);
-}
-
-__device__ __forceinline__ uint64_t dispatch_tag() {
-    const uint64_t q = (uint64_t)__builtin_amdgcn_queue_ptr();
-    return fni8_llvm_dispatch_id() ^ (q * 0x9E3779B97F4A7C15ull);
-}
-
-// Atomic read of a flag word, executed in the L2 of this XCD.  Waits for every
-// vector memory operation of the wave.
-__device__ __forceinline__ uint64_t poll_flag(const uint64_t* p) {
-    uint64_t v;
-    const uint64_t zero = 0;
-    asm volatile("global_atomic_or_x2 %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)"
-                 : "=v"(v) : "v"(p), "v"(zero) : "memory");
-    return v;
-}
 
 // Load the fp16 chunks of token rows r0 .. r0+nr-1 (thread tid: chunk tid + i*NT).
 template <int WAVES, int XCH, int NR>
@@ -158,9 +139,7 @@ __device__ __forceinline__ void produce_rows(const uint4 (&xv)[NR][XCH], int r0,
     // global stores.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (tid < nr)
-        __hip_atomic_store(flags + (r0 + tid) * kFlagStride, tag, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (tid < nr) publish_flag(flags + (r0 + tid) * kFlagStride, tag);
 }
 
 // NB: 16-row MFMA blocks; RB: 8-row load groups (the workgroup's weight rows
@@ -375,7 +354,7 @@ int launch_coop(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, c
     const unsigned nblk = (unsigned)((N + 8 * RB - 1) / (8 * RB));
     hipLaunchKernelGGL(kern, dim3(kXcds * M + nblk), dim3(WAVES * 64), lds, st, x, ldx, M, K, w,
                        ws, N, bias, y, ldy, xq_out, xs_out, acc_out, work, region_bytes,
-                       (uint64_t)__atomic_load_n(&g_wait_ticks, __ATOMIC_RELAXED));
+                       fni8h::xcd_wait_ticks());
     return FNI8_OK;
 }
 
@@ -386,6 +365,8 @@ namespace fni8h {
 void set_coop_wait_ticks(int64_t ticks) {
     __atomic_store_n(&g_wait_ticks, ticks < 0 ? kWaitTicks : ticks, __ATOMIC_RELAXED);
 }
+
+uint64_t xcd_wait_ticks() { return (uint64_t)__atomic_load_n(&g_wait_ticks, __ATOMIC_RELAXED); }
 
 // Zero for shapes the one-launch path does not take, so callers allocate
 // nothing for them.

@@ -339,6 +339,154 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
                                        bias, y, ldy, acc_out);
 }
 
+// ---- fp16 activations, M <= 4, quantized slab by slab in the weight stream -----
+// The fused kernel above quantizes the wave's whole share in the prologue,
+// before its weight stream can start to be consumed.  Here the prologue keeps
+// only the row maxima: slab t of the wave's share is held as one 16-byte chunk
+// per lane (lane l: token l/16, elements (l%16)*8 .. +8 of the slab), and it is
+// quantized into the A-operand area just before the MFMAs that read it, so the
+// quantization's VALU work runs while later weight batches are in flight.
+// PER = 4*PQ slabs per wave (K = 512 * WAVES * PQ).
+template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, bool EB = false>
+__global__ __launch_bounds__(WAVES * 64) void decode_mfma_jit_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int M, int K, const int8_t* __restrict__ w,
+    const float* __restrict__ ws, int N, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ y, int64_t ldy, int8_t* __restrict__ xq_out,
+    float* __restrict__ xs_out, int32_t* __restrict__ acc_out) {
+    constexpr int MM = 4;                  // token rows: 64 lanes = 4 rows x 16 chunks of a slab
+    constexpr int ROWS = 16 * NB;
+    constexpr int TILE = ROWS * 128;
+    constexpr int PER = 4 * PQ;            // slabs per wave
+    constexpr int NBT = PER / SB;          // batches per wave
+    constexpr int XAREA = PER * MM * 128;  // the wave's int8 activations: [PER][MM tokens][128]
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    int8_t* tiles = smem;                                     // [WAVES][SB][TILE]
+    int8_t* xarea = smem + WAVES * SB * TILE;                 // [WAVES][XAREA]
+    uint32_t* amx = reinterpret_cast<uint32_t*>(xarea + WAVES * XAREA);  // [WAVES][MM]
+    float* scl = reinterpret_cast<float*>(amx + WAVES * MM);  // [MM]
+    i32x4* red = reinterpret_cast<i32x4*>(smem);              // after the main loop
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = blockIdx.x * (8 * RB);
+    const int s0 = wave * PER;
+    const int r = lane & 15, g = lane >> 4;
+    const int xm = lane >> 4, xc = lane & 15;  // this lane's token and 8-element chunk of a slab
+    const bool xlive = xm < M;
+
+    // 1. this lane's chunk of every slab of the share (activation loads first)
+    uint4 xv[PER];
+    const uint16_t* xrow = x + (int64_t)(xlive ? xm : 0) * ldx + (int64_t)s0 * 128 + xc * 8;
+#pragma unroll
+    for (int t = 0; t < PER; t++)
+        xv[t] = xlive ? *reinterpret_cast<const uint4*>(xrow + t * 128) : make_uint4(0, 0, 0, 0);
+    // 2. first weight batch
+    WeightLanes<NB, RB> wl;
+    wl.init(w, n0, N, K, s0, lane);
+    i32x4 wa[SB][RB], wb[SB][RB];
+#pragma unroll
+    for (int j = 0; j < SB; j++)
+#pragma unroll
+        for (int h = 0; h < RB; h++) wa[j][h] = ld16_nt(wl.src[h] + (int64_t)j * 128);
+
+    // 3. row maxima: over the lane's chunks, then its 16-lane group (one token),
+    //    then across the waves
+    uint32_t mx = 0;
+#pragma unroll
+    for (int t = 0; t < PER; t++) mx = fni8::amax_chunk(mx, xv[t]);
+    {
+        int v = (int)fni8::amax_fold(mx), o;
+        o = fni8::dpp<fni8::kDppXor1>(v); v = o > v ? o : v;
+        o = fni8::dpp<fni8::kDppXor2>(v); v = o > v ? o : v;
+        o = fni8::dpp<fni8::kDppHalfMirror>(v); v = o > v ? o : v;
+        o = fni8::dpp<fni8::kDppMirror>(v); v = o > v ? o : v;
+        if (xc == 0) amx[wave * MM + xm] = (uint32_t)v;
+    }
+    lds_barrier();
+    if constexpr (EB && NBT > 1) {
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < RB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)(SB + j) * 128);
+    }
+    uint32_t a = amx[xm];
+#pragma unroll
+    for (int wv = 1; wv < WAVES; wv++) a = amx[wv * MM + xm] > a ? amx[wv * MM + xm] : a;
+    const float sc = fni8::row_scale_from_bits(a);
+    const bool live = xlive && __builtin_isfinite(sc);  // NaN/inf scale: every q is 0
+    const float yr = 1.0f / sc;                          // correctly rounded (build flag)
+    if (wave == 0 && xc == 0) {
+        scl[xm] = sc;
+        if (blockIdx.x == 0 && xlive) xs_out[xm] = sc;
+    }
+    int8_t* xw = xarea + wave * XAREA;
+    const int xoff = xm * 128 + swz(xm, xc >> 1) + (xc & 1) * 8;  // in a slab's [MM][128]
+    const int tok = r < M ? r : M - 1;  // tokens past M repeat M-1 (never stored)
+    int aoff[2];
+#pragma unroll
+    for (int q = 0; q < 2; q++) aoff[q] = tok * 128 + swz(tok, 4 * q + g);
+
+    // 4. the weight stream, each slab's activations quantized just before use
+    i32x4 acc[2][1][NB];
+#pragma unroll
+    for (int q = 0; q < 2; q++)
+#pragma unroll
+        for (int b = 0; b < NB; b++) acc[q][0][b] = i32x4{0, 0, 0, 0};
+    int8_t* st = tiles + wave * (SB * TILE);
+    auto compute = [&](const i32x4 (&wv)[SB][RB], int bt) {
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+            const int t = bt * SB + j;
+            const uint2 q = fni8::quant_chunk(xv[t], sc, yr, live);
+            *reinterpret_cast<uint2*>(xw + t * (MM * 128) + xoff) = q;
+            if (blockIdx.x == 0 && xlive)
+                *reinterpret_cast<uint2*>(xq_out + (int64_t)xm * K + (int64_t)(s0 + t) * 128 + xc * 8) = q;
+#pragma unroll
+            for (int h = 0; h < RB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + wl.woff[h]) = wv[j][h];
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int j = 0; j < SB; j++) {
+            const int8_t* xs_ = xw + (bt * SB + j) * (MM * 128);
+            const i32x4 a0 = ld16(xs_ + aoff[0]), a1 = ld16(xs_ + aoff[1]);
+            i32x4 bf[NB][2];
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+#pragma unroll
+                for (int q = 0; q < 2; q++) bf[b][q] = *reinterpret_cast<const i32x4*>(st + j * TILE + wl.roff[b][q]);
+#pragma unroll
+            for (int b = 0; b < NB; b++) {
+                acc[0][0][b] = fni8::mfma_i8(a0, bf[b][0], acc[0][0][b]);
+                acc[1][0][b] = fni8::mfma_i8(a1, bf[b][1], acc[1][0][b]);
+            }
+        }
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("" ::: "memory");
+    };
+#pragma unroll
+    for (int bt = 0; bt < NBT - 1; bt++) {
+        if (!EB || bt > 0) {
+#pragma unroll
+            for (int j = 0; j < SB; j++)
+#pragma unroll
+                for (int h = 0; h < RB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)((bt + 1) * SB + j) * 128);
+        }
+        compute(wa, bt);
+#pragma unroll
+        for (int j = 0; j < SB; j++)
+#pragma unroll
+            for (int h = 0; h < RB; h++) wa[j][h] = wb[j][h];
+    }
+    compute(wa, NBT - 1);
+
+    __syncthreads();  // the reduction area overlaps the tiles
+    reduce_store<1, NB, WAVES, 8 * RB>(acc, red, wave, lane, tid, n0, 0, M, N, scl, nullptr, ws,
+                                       bias, y, ldy, acc_out);
+}
+
 template <int MT, int NB, int WAVES, int SB, bool GROUPED = false, int RB = 2 * NB>
 int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const int8_t* w,
            const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
@@ -381,6 +529,30 @@ int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, 
         return 1;
     } else {
         auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ, RB, MM, EB>;
+        static const bool ok = hipFuncSetAttribute((const void*)kern,
+                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                   160 * 1024) == hipSuccess;
+        if (!ok) return 1;
+        hipLaunchKernelGGL(kern, dim3((unsigned)((N + 8 * RB - 1) / (8 * RB))), dim3(WAVES * 64),
+                           lds, st, x, ldx, M, K, w, ws, N, bias, y, ldy, xq_out, xs_out, acc_out);
+        return FNI8_OK;
+    }
+}
+
+template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, bool EB = false>
+int launch_jit(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, const float* ws,
+               int N, const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
+               float* xs_out, int32_t* acc_out, hipStream_t st) {
+    static_assert((4 * PQ) % SB == 0, "batches must divide the share");
+    if (K != 512 * WAVES * PQ || M > 4) return 1;
+    constexpr size_t tiles = (size_t)WAVES * SB * 16 * NB * 128;
+    constexpr size_t lds_main = tiles + (size_t)WAVES * 4 * PQ * 512 + WAVES * 16 + 16;
+    constexpr size_t red = (size_t)WAVES * NB * 64 * 16;
+    constexpr size_t lds = lds_main > red ? lds_main : red;
+    if constexpr (lds > 160 * 1024) {
+        return 1;
+    } else {
+        auto kern = decode_mfma_jit_kernel<NB, WAVES, SB, PQ, RB, EB>;
         static const bool ok = hipFuncSetAttribute((const void*)kern,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    160 * 1024) == hipSuccess;
@@ -478,12 +650,21 @@ int launch_grouped_mt(const int8_t* xq, int64_t ldx, const float* xs, const int3
 int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w,
                        const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
                        int8_t* xq_out, float* xs_out, int32_t* acc_out, hipStream_t st) {
+#ifndef FNI8_FUSED_JIT
 #define FNI8_DF_RBE(NB, WV, SB, PQ, RB, EB)                                                     \
     do {                                                                                        \
         const int rc = launch_fused<NB, WV, SB, PQ, RB, 4, EB>(x, ldx, M, K, w, ws, N, bias, y, \
                                                                ldy, xq_out, xs_out, acc_out, st); \
         if (rc != 1) return rc;                                                                 \
     } while (0)
+#else
+#define FNI8_DF_RBE(NB, WV, SB, PQ, RB, EB)                                                     \
+    do {                                                                                        \
+        const int rc = launch_jit<NB, WV, SB, PQ, RB, EB>(x, ldx, M, K, w, ws, N, bias, y,      \
+                                                          ldy, xq_out, xs_out, acc_out, st);    \
+        if (rc != 1) return rc;                                                                 \
+    } while (0)
+#endif
 #define FNI8_DF_RB(NB, WV, SB, PQ, RB) FNI8_DF_RBE(NB, WV, SB, PQ, RB, false)
 #define FNI8_DF(NB, WV, SB, PQ) FNI8_DF_RB(NB, WV, SB, PQ, 2 * NB)
     const bool wide = N >= 16384, narrow = N <= 4096;

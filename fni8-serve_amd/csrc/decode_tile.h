@@ -12,7 +12,54 @@
 
 #include "common.h"
 
+extern "C" __device__ uint64_t fni8_llvm_dispatch_id() __asm("llvm.amdgcn.dispatch.id");
+
 namespace fni8dec {
+
+// ---- exchange between the workgroups of one XCD -------------------------------
+// The 8 XCDs of MI355X each have their own L2, shared by that XCD's CUs, and
+// not kept coherent with the other XCDs' L2s inside a kernel.  Workgroups of
+// one XCD can therefore hand data to each other through their L2: the writer
+// stores the data, waits until every store is acknowledged by the L2, then
+// stores a flag; the reader polls the flag with an atomic (atomics execute in
+// the L2; a plain load, even after a workgroup-scope L1 invalidate, kept
+// returning a stale flag from the reader's L1) and then loads the data, which
+// no workgroup of the kernel read before the flag was set, so no L1 holds a
+// stale copy (the L1 is invalidated at every kernel start).  Both sides check
+// the XCD they run on with xcc_id(); a flag holds dispatch_tag(), so a flag left
+// by an earlier launch never matches and the memory needs no reset.
+
+// Index (0..7) of the XCD this wave runs on.
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+    return v & 7u;
+}
+
+// A value no earlier dispatch produced: the dispatch id (the AQL packet index,
+// strictly increasing per queue and new on every graph replay) mixed with the
+// queue's address.
+__device__ __forceinline__ uint64_t dispatch_tag() {
+    const uint64_t q = (uint64_t)__builtin_amdgcn_queue_ptr();
+    return fni8_llvm_dispatch_id() ^ (q * 0x9E3779B97F4A7C15ull);
+}
+
+// Atomic read of a flag word, executed in the L2 of this XCD.  Waits for every
+// vector memory operation of the wave.
+__device__ __forceinline__ uint64_t poll_flag(const uint64_t* p) {
+    uint64_t v;
+    const uint64_t zero = 0;
+    asm volatile("global_atomic_or_x2 %0, %1, %2, off sc0\n\ts_waitcnt vmcnt(0)"
+                 : "=v"(v) : "v"(p), "v"(zero) : "memory");
+    return v;
+}
+
+// Store a flag once this wave's earlier global stores are acknowledged by the
+// L2 (the caller makes the other waves' stores complete first, e.g. with
+// s_waitcnt vmcnt(0) in every wave and a barrier).
+__device__ __forceinline__ void publish_flag(uint64_t* p, uint64_t tag) {
+    __hip_atomic_store(p, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
 __device__ __forceinline__ i32x4 ld16(const void* p) {
     return *reinterpret_cast<const i32x4*>(p);

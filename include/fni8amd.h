@@ -110,10 +110,9 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
  * fni8_linear_w8a8_f16 with a workspace: the same call, arithmetic and
  * outputs (bit for bit), in one launch instead of two where that measured
  * faster -- 5 <= M <= 16 tokens on QKV- and down-shaped weights, 5 <= M <= 8
- * on O-shaped ones
- * (replaces fni8serve/layers/linear.py:69 at decode batch sizes).  The
- * per-token quantization then runs once per XCD and reaches the GEMM
- * workgroups through that XCD's L2; `workspace` holds the exchanged rows.
+ * on O-shaped ones (replaces fni8serve/layers/linear.py:69 at decode batch
+ * sizes).  The per-token quantization then runs once per XCD and reaches the
+ * GEMM workgroups through that XCD's L2; `workspace` holds the exchanged rows.
  * Other shapes take the same launches as fni8_linear_w8a8_f16.
  *   workspace        device memory, 256-byte aligned, at least
  *                    fni8_linear_workspace_bytes(M, N, K) bytes; any contents

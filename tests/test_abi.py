@@ -142,17 +142,16 @@ def test_moe_route_argument_errors(lib):
 
 def test_workspace_size_and_argument_checks(lib):
     """The one-launch path's workspace: 8 regions of (2304 + M*K rounded up to
-    256) bytes for the shapes it takes (5 <= M <= 16; QKV-, O- and down-shaped
-    weights), none otherwise; a misaligned workspace is an argument error
-    raised before any launch."""
+    256) bytes for the shapes it takes (5..16 tokens on QKV- and down-shaped
+    weights, 5..8 on O-shaped ones), none otherwise; a misaligned workspace is
+    an argument error raised before any launch."""
     for M, N, K in ((5, 4096, 4096), (8, 4096, 4096), (16, 6144, 4096), (7, 4096, 12288),
                     (8, 100, 4096), (16, 4096, 12288)):
         assert lib.fni8_linear_workspace_bytes(M, N, K) == 8 * (2304 + ((M * K + 255) // 256) * 256)
     assert lib.fni8_linear_workspace_bytes(16, 4096, 12288) == 1591296
     for M, N, K in ((0, 4096, 4096), (1, 4096, 4096), (4, 4096, 4096), (9, 4096, 4096),
-                    (17, 6144, 4096),
-                    (64, 4096, 4096), (16, 24576, 4096), (16, 6144, 12288), (16, 4096, 1024),
-                    (16, 4096, 8192)):
+                    (17, 6144, 4096), (64, 4096, 12288), (16, 24576, 4096), (16, 6144, 12288),
+                    (16, 4096, 1024), (16, 4096, 8192)):
         assert lib.fni8_linear_workspace_bytes(M, N, K) == 0, (M, N, K)
     P = ctypes.c_void_p
     fake = P(0x1000)

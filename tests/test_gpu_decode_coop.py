@@ -227,3 +227,4 @@ def test_small_and_ragged_N(pkg, wl, lib, cuda, N):
     ref = _call(lib, x, qt, None, None, acc=True)
     torch.cuda.synchronize()
     assert _same(got, ref)
+
