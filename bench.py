@@ -133,8 +133,9 @@ def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
     """HIP-event timing of the decode linear (M <= 16): for each (linear, M), one
     burst of its 36 per-layer calls between two events on the launch stream.
     For M <= 4 a call is one launch (quantization fused: the dot4 GEMV at M = 1,
-    the MFMA kernel at M = 4); for M = 16 it is the quantize launch plus the
-    MFMA GEMM launch.  Every burst is
+    the MFMA kernel at M = 4); for M = 16 it is one launch on QKV and down (the
+    quantization shared per XCD) and the quantize launch plus the MFMA GEMM
+    launch on O and gate_up.  Every burst is
     enqueued behind a GPU-side sleep, so the events bracket back-to-back kernel
     execution with no host gaps; the per-call mean of such bursts agrees with
     rocprofv3's kernel durations."""
@@ -183,7 +184,8 @@ def kernel_roofline(pkg, wl, pool, device, ms=(1, 4, 16), reps=2):
     r = {
         "kernel": "decode W8A8 linear, M <= 16: one launch with the quantization fused for "
                   "M <= 4 (decode_gemv_kernel at M = 1, decode_mfma_fused_kernel at M = 4); "
-                  "quant_rowwise_regs_kernel + decode_mfma_kernel for M = 16",
+                  "at M = 16 decode_coop_kernel (one launch) for QKV and down, "
+                  "quant_rowwise_regs_kernel + decode_mfma_kernel for O and gate_up",
         "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
         "avg_launch_us": round(tot_t / n_launch * 1e6, 3),

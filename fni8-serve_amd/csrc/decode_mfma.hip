@@ -27,12 +27,13 @@
 // Fused quantization (decode_mfma_fused_kernel, M <= 4): every workgroup reads
 // the M fp16 rows of x (each wave its own K share, 1 KB per load instruction),
 // reduces each row's max magnitude (DPP, then one barrier across the waves),
-// and quantizes its share into a wave-private int8 area of LDS that feeds the
-// A operand for the whole K loop.  The loads of the first weight batch are
-// issued before all of this, so the quantization runs while they are in
-// flight.  Each workgroup quantizes the rows for itself (no workgroup waits
-// for another); on MFMA the dot products cost no VALU time, which is what made
-// the dot4 GEMV slow at M = 4.
+// then, slab by slab inside the weight stream, quantizes its share into a
+// wave-private int8 area of LDS that feeds the A operand of that slab's MFMAs.
+// The loads of the first weight batch are issued before the maxima, so the
+// prologue runs while they are in flight, and the quantization's VALU work
+// overlaps the later batches.  Each workgroup quantizes the rows for itself (no
+// workgroup waits for another); on MFMA the dot products cost no VALU time,
+// which is what made the dot4 GEMV slow at M = 4.
 #include "decode_tile.h"
 
 namespace {
@@ -177,178 +178,18 @@ __global__ __launch_bounds__(WAVES * 64) void decode_mfma_kernel(
                                 GROUPED ? rmap : nullptr, ws, bias, y, ldy, acc_out);
 }
 
-// ---- fp16 activations, M <= MM, quantized in the kernel --------------------
-// MM (4, 8 or 16): token rows of the int8 activation area; the MFMA A operand
-// has 16 rows, tokens past M repeat token M-1 (computed, never stored).
-// PQ: each wave's K share is 4*PQ slabs (K = 512 * WAVES * PQ exactly), which
-// makes every loop trip count a compile-time constant.
-// The lane's fp16 chunks stay in registers between the max and the quantize
-// pass when there are at most 16 of them (MM * PQ <= 16); otherwise the
-// quantize pass loads them again (from cache: the max pass just read them).
-// EB: the second weight batch is issued after the row-max barrier, before the
-// quantization, so its latency overlaps the quantization's VALU work.
-template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, int MM = 4, bool EB = false>
-__global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
-    const uint16_t* __restrict__ x, int64_t ldx, int M, int K, const int8_t* __restrict__ w,
-    const float* __restrict__ ws, int N, const uint16_t* __restrict__ bias,
-    uint16_t* __restrict__ y, int64_t ldy, int8_t* __restrict__ xq_out,
-    float* __restrict__ xs_out, int32_t* __restrict__ acc_out) {
-    constexpr int ROWS = 16 * NB;
-    constexpr int TILE = ROWS * 128;
-    constexpr int PER = 4 * PQ;            // slabs per wave
-    constexpr int NBT = PER / SB;          // batches per wave
-    constexpr int XAREA = PER * MM * 128;  // the wave's int8 activations: [PER][MM tokens][128]
-    constexpr bool KEEP = MM * PQ <= 16;   // fp16 chunks kept in registers between passes
-    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
-    int8_t* tiles = smem;                                     // [WAVES][SB][TILE]
-    int8_t* xarea = smem + WAVES * SB * TILE;                 // [WAVES][XAREA]
-    uint32_t* amx = reinterpret_cast<uint32_t*>(xarea + WAVES * XAREA);  // [WAVES][MM]
-    float* scl = reinterpret_cast<float*>(amx + WAVES * MM);  // [MM]
-    i32x4* red = reinterpret_cast<i32x4*>(smem);              // after the main loop
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = blockIdx.x * (8 * RB);
-    const int s0 = wave * PER;
-    const int r = lane & 15, g = lane >> 4;
-
-    // chunk j of this lane: token j / PQ, elements s0*128 + ((j % PQ) * 64 + lane) * 8 .. + 8
-    auto xchunk = [&](int j) -> uint4 {
-        const int m = j / PQ;
-        if (m < M)
-            return *reinterpret_cast<const uint4*>(x + (int64_t)m * ldx + (int64_t)s0 * 128 +
-                                                   ((j % PQ) * 64 + lane) * 8);
-        return make_uint4(0, 0, 0, 0);
-    };
-    // 1. activation loads first (the compiler then waits for them without
-    //    waiting for the weight loads issued after)
-    uint4 xv[KEEP ? MM * PQ : 1];
-    if constexpr (KEEP) {
-#pragma unroll
-        for (int j = 0; j < MM * PQ; j++) xv[j] = xchunk(j);
-    }
-    // 2. first weight batch
-    WeightLanes<NB, RB> wl;
-    wl.init(w, n0, N, K, s0, lane);
-    i32x4 wa[SB][RB], wb[SB][RB];
-#pragma unroll
-    for (int j = 0; j < SB; j++)
-#pragma unroll
-        for (int h = 0; h < RB; h++) wa[j][h] = ld16_nt(wl.src[h] + (int64_t)j * 128);
-
-    // 3. row max magnitudes: integer max over (bits & 0x7fff), one wave-uniform
-    //    value per token, then across the waves
-#pragma unroll
-    for (int m = 0; m < MM; m++) {
-        uint32_t mx = 0;
-#pragma unroll
-        for (int jj = 0; jj < PQ; jj++) mx = fni8::amax_chunk(mx, KEEP ? xv[m * PQ + jj] : xchunk(m * PQ + jj));
-        mx = fni8::wave_max_uniform(fni8::amax_fold(mx));
-        if (lane == 0) amx[wave * MM + m] = mx;
-    }
-    lds_barrier();
-    if constexpr (EB && NBT > 1) {
-#pragma unroll
-        for (int j = 0; j < SB; j++)
-#pragma unroll
-            for (int h = 0; h < RB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)(SB + j) * 128);
-    }
-    // 4. quantize this wave's share into its LDS area: token rows of 128 bytes per
-    //    slab, 16-byte chunks swizzled by token (conflict-free A-operand reads)
-    int8_t* xw = xarea + wave * XAREA;
-#pragma unroll
-    for (int m = 0; m < MM; m++) {
-        uint32_t a = amx[m];
-#pragma unroll
-        for (int wv = 1; wv < WAVES; wv++) a = amx[wv * MM + m] > a ? amx[wv * MM + m] : a;
-        const float sc = fni8::row_scale_from_bits(a);
-        const bool live = m < M && __builtin_isfinite(sc);  // NaN/inf scale: every q is 0
-        const float yr = 1.0f / sc;                          // correctly rounded (build flag)
-        if (wave == 0 && lane == 0) {
-            scl[m] = sc;
-            if (blockIdx.x == 0 && m < M) xs_out[m] = sc;
-        }
-        if (m >= M) continue;
-#pragma unroll
-        for (int jj = 0; jj < PQ; jj++) {
-            const int kl = (jj * 64 + lane) * 8;  // element offset in the share
-            const uint2 q = fni8::quant_chunk(KEEP ? xv[m * PQ + jj] : xchunk(m * PQ + jj), sc, yr, live);
-            *reinterpret_cast<uint2*>(xw + ((kl >> 7) * MM + m) * 128 + swz(m, (kl & 127) >> 4) +
-                                      (kl & 15)) = q;
-            if (blockIdx.x == 0)
-                *reinterpret_cast<uint2*>(xq_out + (int64_t)m * K + (int64_t)s0 * 128 + kl) = q;
-        }
-    }
-    const int tok = r < M ? r : M - 1;  // tokens past M repeat M-1 (never stored)
-    int aoff[2];
-#pragma unroll
-    for (int q = 0; q < 2; q++) aoff[q] = tok * 128 + swz(tok, 4 * q + g);
-
-    // 5. the weight stream
-    i32x4 acc[2][1][NB];
-#pragma unroll
-    for (int q = 0; q < 2; q++)
-#pragma unroll
-        for (int b = 0; b < NB; b++) acc[q][0][b] = i32x4{0, 0, 0, 0};
-    int8_t* st = tiles + wave * (SB * TILE);
-    auto compute = [&](const i32x4 (&wv)[SB][RB], int bt) {
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < SB; j++)
-#pragma unroll
-            for (int h = 0; h < RB; h++) *reinterpret_cast<i32x4*>(st + j * TILE + wl.woff[h]) = wv[j][h];
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int j = 0; j < SB; j++) {
-            const int8_t* xs_ = xw + (bt * SB + j) * (MM * 128);
-            const i32x4 a0 = ld16(xs_ + aoff[0]), a1 = ld16(xs_ + aoff[1]);
-            i32x4 bf[NB][2];
-#pragma unroll
-            for (int b = 0; b < NB; b++)
-#pragma unroll
-                for (int q = 0; q < 2; q++) bf[b][q] = *reinterpret_cast<const i32x4*>(st + j * TILE + wl.roff[b][q]);
-#pragma unroll
-            for (int b = 0; b < NB; b++) {
-                acc[0][0][b] = fni8::mfma_i8(a0, bf[b][0], acc[0][0][b]);
-                acc[1][0][b] = fni8::mfma_i8(a1, bf[b][1], acc[1][0][b]);
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-        asm volatile("" ::: "memory");
-    };
-#pragma unroll
-    for (int bt = 0; bt < NBT - 1; bt++) {
-        if (!EB || bt > 0) {
-#pragma unroll
-            for (int j = 0; j < SB; j++)
-#pragma unroll
-                for (int h = 0; h < RB; h++) wb[j][h] = ld16_nt(wl.src[h] + (int64_t)((bt + 1) * SB + j) * 128);
-        }
-        compute(wa, bt);
-#pragma unroll
-        for (int j = 0; j < SB; j++)
-#pragma unroll
-            for (int h = 0; h < RB; h++) wa[j][h] = wb[j][h];
-    }
-    compute(wa, NBT - 1);
-
-    __syncthreads();  // the reduction area overlaps the tiles
-    reduce_store<1, NB, WAVES, 8 * RB>(acc, red, wave, lane, tid, n0, 0, M, N, scl, nullptr, ws,
-                                       bias, y, ldy, acc_out);
-}
-
-// ---- fp16 activations, M <= 4, quantized slab by slab in the weight stream -----
-// The fused kernel above quantizes the wave's whole share in the prologue,
-// before its weight stream can start to be consumed.  Here the prologue keeps
-// only the row maxima: slab t of the wave's share is held as one 16-byte chunk
-// per lane (lane l: token l/16, elements (l%16)*8 .. +8 of the slab), and it is
-// quantized into the A-operand area just before the MFMAs that read it, so the
-// quantization's VALU work runs while later weight batches are in flight.
-// PER = 4*PQ slabs per wave (K = 512 * WAVES * PQ).
+// ---- fp16 activations, M <= 4, quantized in the kernel, slab by slab ---------
+// The prologue keeps only the row maxima: slab t of the wave's share is held as
+// one 16-byte chunk per lane (lane l: token l/16, elements (l%16)*8 .. +8 of
+// the slab), and it is quantized into the A-operand area just before the MFMAs
+// that read it, so the quantization's VALU work runs while later weight batches
+// are in flight.  (Quantizing the whole share in the prologue instead, before
+// the weight stream could be consumed, measured 2-11% slower: M = 4, QKV 7.99
+// against 7.11 us, down 12.21 against 11.29.)  PER = 4*PQ slabs per wave
+// (K = 512 * WAVES * PQ).  EB: the second weight batch is issued right after
+// the row-max barrier.
 template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, bool EB = false>
-__global__ __launch_bounds__(WAVES * 64) void decode_mfma_jit_kernel(
+__global__ __launch_bounds__(WAVES * 64) void decode_mfma_fused_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, int M, int K, const int8_t* __restrict__ w,
     const float* __restrict__ ws, int N, const uint16_t* __restrict__ bias,
     uint16_t* __restrict__ y, int64_t ldy, int8_t* __restrict__ xq_out,
@@ -514,33 +355,8 @@ int launch(const int8_t* xq, int64_t ldx, const float* xs, int M, int K, const i
     return FNI8_OK;
 }
 
-template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, int MM = 4, bool EB = false>
-int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, const float* ws,
-                 int N, const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
-                 float* xs_out, int32_t* acc_out, hipStream_t st) {
-    static_assert((4 * PQ) % SB == 0, "batches must divide the share");
-    static_assert(MM == 4 || MM == 8 || MM == 16, "token rows of the activation area");
-    if (K != 512 * WAVES * PQ || M > MM) return 1;
-    constexpr size_t tiles = (size_t)WAVES * SB * 16 * NB * 128;
-    constexpr size_t lds_main = tiles + (size_t)WAVES * MM * PQ * 512 + WAVES * MM * 4 + MM * 4;
-    constexpr size_t red = (size_t)WAVES * NB * 64 * 16;
-    constexpr size_t lds = lds_main > red ? lds_main : red;
-    if constexpr (lds > 160 * 1024) {
-        return 1;
-    } else {
-        auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ, RB, MM, EB>;
-        static const bool ok = hipFuncSetAttribute((const void*)kern,
-                                                   hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                   160 * 1024) == hipSuccess;
-        if (!ok) return 1;
-        hipLaunchKernelGGL(kern, dim3((unsigned)((N + 8 * RB - 1) / (8 * RB))), dim3(WAVES * 64),
-                           lds, st, x, ldx, M, K, w, ws, N, bias, y, ldy, xq_out, xs_out, acc_out);
-        return FNI8_OK;
-    }
-}
-
 template <int NB, int WAVES, int SB, int PQ, int RB = 2 * NB, bool EB = false>
-int launch_jit(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, const float* ws,
+int launch_fused(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, const float* ws,
                int N, const uint16_t* bias, uint16_t* y, int64_t ldy, int8_t* xq_out,
                float* xs_out, int32_t* acc_out, hipStream_t st) {
     static_assert((4 * PQ) % SB == 0, "batches must divide the share");
@@ -552,7 +368,7 @@ int launch_jit(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w, co
     if constexpr (lds > 160 * 1024) {
         return 1;
     } else {
-        auto kern = decode_mfma_jit_kernel<NB, WAVES, SB, PQ, RB, EB>;
+        auto kern = decode_mfma_fused_kernel<NB, WAVES, SB, PQ, RB, EB>;
         static const bool ok = hipFuncSetAttribute((const void*)kern,
                                                    hipFuncAttributeMaxDynamicSharedMemorySize,
                                                    160 * 1024) == hipSuccess;
@@ -650,35 +466,26 @@ int launch_grouped_mt(const int8_t* xq, int64_t ldx, const float* xs, const int3
 int launch_fused_table(const uint16_t* x, int64_t ldx, int M, int K, const int8_t* w,
                        const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
                        int8_t* xq_out, float* xs_out, int32_t* acc_out, hipStream_t st) {
-#ifndef FNI8_FUSED_JIT
-#define FNI8_DF_RBE(NB, WV, SB, PQ, RB, EB)                                                     \
-    do {                                                                                        \
-        const int rc = launch_fused<NB, WV, SB, PQ, RB, 4, EB>(x, ldx, M, K, w, ws, N, bias, y, \
-                                                               ldy, xq_out, xs_out, acc_out, st); \
-        if (rc != 1) return rc;                                                                 \
+#define FNI8_DF_RBE(NB, WV, SB, PQ, RB, EB)                                                  \
+    do {                                                                                     \
+        const int rc = launch_fused<NB, WV, SB, PQ, RB, EB>(x, ldx, M, K, w, ws, N, bias, y, \
+                                                            ldy, xq_out, xs_out, acc_out, st); \
+        if (rc != 1) return rc;                                                              \
     } while (0)
-#else
-#define FNI8_DF_RBE(NB, WV, SB, PQ, RB, EB)                                                     \
-    do {                                                                                        \
-        const int rc = launch_jit<NB, WV, SB, PQ, RB, EB>(x, ldx, M, K, w, ws, N, bias, y,      \
-                                                          ldy, xq_out, xs_out, acc_out, st);    \
-        if (rc != 1) return rc;                                                                 \
-    } while (0)
-#endif
 #define FNI8_DF_RB(NB, WV, SB, PQ, RB) FNI8_DF_RBE(NB, WV, SB, PQ, RB, false)
 #define FNI8_DF(NB, WV, SB, PQ) FNI8_DF_RB(NB, WV, SB, PQ, 2 * NB)
+    // Measured at 3 and 4 tokens over the Qwen3-8B linears (36 layers of
+    // distinct weights; six launch tables, every variant bit-identical).
     const bool wide = N >= 16384, narrow = N <= 4096;
     if (wide) {
         FNI8_DF(2, 4, 2, 2);
         FNI8_DF(2, 8, 1, 3);
     } else if (narrow) {
-        // second weight batch issued before the quantization (O and down at 3-4
-        // tokens: 6.81 -> 6.23 and 12.88 -> 11.82 us; even or slower on QKV and
-        // gate_up, which keep the later issue)
-        FNI8_DF_RBE(1, 4, 4, 2, 2, true);
-        FNI8_DF_RBE(1, 8, 3, 3, 2, true);
+        // second weight batch issued right after the row maxima (O and down)
+        FNI8_DF_RBE(1, 4, 2, 2, 2, true);
+        FNI8_DF_RBE(1, 8, 2, 3, 2, true);
     } else {
-        if (prefer_24_rows(N)) FNI8_DF_RB(2, 8, 2, 1, 3);  // QKV: 24-row workgroups
+        if (prefer_24_rows(N)) FNI8_DF_RB(2, 4, 2, 2, 3);  // QKV: 24-row workgroups
         FNI8_DF(2, 8, 1, 1);
         FNI8_DF(2, 8, 1, 3);
     }
