@@ -27,6 +27,7 @@ SIGNATURES = {
     "fni8_init": [],
     "fni8_quantize_rowwise_f16": [_P, _I, _I, _I, _P, _I, _P, _P],
     "fni8_gemm_w8a8": [_P, _I, _P, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P],
+    "fni8_gemm_w8a8_ws": [_P, _I, _P, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _I, _P],
     "fni8_linear_w8a8_f16": [_P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P],
     "fni8_linear_w8a8_f16_ws": [_P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P],
     "fni8_linear_w8a8_f16_noalloc": [_P, _I, _I, _I, _P, _P, _I, _P, _P, _I, _P],
@@ -44,7 +45,7 @@ SIGNATURES = {
 }
 STRING_FUNCS = ("fni8_strerror", "fni8_last_error", "fni8_version")
 INT64_FUNCS = {"fni8_linear_workspace_bytes": [_I, _I, _I]}
-VOID_FUNCS = {"fni8_debug_coop_wait_ticks": [_I]}
+VOID_FUNCS = {"fni8_debug_coop_wait_ticks": [_I], "fni8_debug_gemm_plan": [_I, _I, _I]}
 
 _lib = None
 _lock = threading.Lock()
@@ -95,7 +96,8 @@ def call(name: str, *args) -> None:
 
 
 def workspace_bytes(M: int, N: int, K: int) -> int:
-    """Workspace bytes fni8_linear_w8a8_f16_ws uses for an [M, K] x [N, K] linear (0: none)."""
+    """Workspace bytes fni8_linear_w8a8_f16_ws / fni8_gemm_w8a8_ws use for an [M, K] x [N, K]
+    product (0: none)."""
     return int(load().fni8_linear_workspace_bytes(M, N, K))
 
 

@@ -287,10 +287,41 @@ int fni8_linear_w8a8_f16_ws(const void* x, int64_t ldx, int64_t M, int64_t K, co
 }
 
 int64_t fni8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-    return fni8h::coop_workspace_bytes(M, N, K);
+    if (M < 0 || N <= 0 || K <= 0 || M >= kMaxDim || N >= kMaxDim || K >= kMaxDim) return 0;
+    if (M <= 16) return fni8h::coop_workspace_bytes(M, N, K);
+    return fni8h::pp_workspace_bytes(M, N, K);
+}
+
+int fni8_gemm_w8a8_ws(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                      const int8_t* w, const float* ws, int64_t N, const void* bias, void* y,
+                      int64_t ldy, int32_t* acc_out, void* workspace, int64_t workspace_bytes,
+                      void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(xq && xs && w && ws && y, FNI8_ERR_NULL, "xq, xs, w, ws and y are required");
+    int rc = check_gemm_shape(M, K, N);
+    if (rc) return rc;
+    REQUIRE(ldq >= K && ldy >= N, FNI8_ERR_STRIDE, "ldq=%lld < K or ldy=%lld < N",
+            (long long)ldq, (long long)ldy);
+    REQUIRE(ldq % 4 == 0 && aligned(xq, 4) && aligned(w, 4), FNI8_ERR_ALIGN,
+            "int8 operands need 4-byte aligned rows");
+    REQUIRE(aligned(xs, 4) && aligned(ws, 4) && aligned(y, 2) && aligned(bias, 2) &&
+                aligned(acc_out, 4),
+            FNI8_ERR_ALIGN, "scale/output pointers misaligned");
+    REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 256)), FNI8_ERR_ALIGN,
+            "workspace must be 256-byte aligned with a size >= 0");
+    rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_gemm(xq, ldq, xs, nullptr, M, K, w, ws, N, 0, nullptr,
+                              (const uint16_t*)bias, (uint16_t*)y, ldy, acc_out,
+                              (hipStream_t)stream, static_cast<int8_t*>(workspace),
+                              workspace ? workspace_bytes : 0);
 }
 
 void fni8_debug_coop_wait_ticks(int64_t ticks) { fni8h::set_coop_wait_ticks(ticks); }
+
+void fni8_debug_gemm_plan(int64_t bm, int64_t bn, int64_t split) {
+    fni8h::set_gemm_plan(bm, bn, split);
+}
 
 int fni8_linear_w8a8_f16_noalloc(const void* x, int64_t ldx, int64_t M, int64_t K,
                                  const int8_t* w, const float* ws, int64_t N, const void* bias,
@@ -312,10 +343,11 @@ int fni8_linear_w8a8_f16_noalloc(const void* x, int64_t ldx, int64_t M, int64_t 
     rc = scratch_address(&sp);
     if (rc) return rc;
     // xq: M rows of K bytes at the start; xs: M floats after the xq area; the
-    // rest of the xq area (past M * K, 256-aligned) is the one-launch path's
-    // workspace.  Every byte the GEMM reads is written by this call's
-    // quantization first, and the workspace needs no clearing, so nothing is
-    // cleared between calls.
+    // rest of the xq area (past M * K, 256-aligned) is the workspace of the
+    // one-launch decode path and of the split-K prefill GEMM (where its plan
+    // fits).  Every byte the GEMM reads is written by this call's quantization
+    // first, and the workspace needs no clearing, so nothing is cleared between
+    // calls.
     const int64_t work_off = (M * K + 255) & ~(int64_t)255;
     return linear_launch(x, ldx, M, K, w, ws, N, bias, y, ldy, sp,
                          reinterpret_cast<float*>(sp + kNoAllocQBytes), nullptr, sp + work_off,
@@ -353,7 +385,8 @@ int linear_launch(const void* x, int64_t ldx, int64_t M, int64_t K, const int8_t
     rc = fni8h::launch_quant_rowwise((const uint16_t*)x, M, K, ldx, xq, K, xs, st);
     if (rc) return rc;
     return fni8h::launch_gemm(xq, K, xs, nullptr, M, K, w, ws, N, 0, nullptr,
-                              (const uint16_t*)bias, (uint16_t*)y, ldy, acc_out, st);
+                              (const uint16_t*)bias, (uint16_t*)y, ldy, acc_out, st, work,
+                              work_bytes);
 }
 
 }  // namespace

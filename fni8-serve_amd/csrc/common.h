@@ -374,10 +374,13 @@ __device__ __forceinline__ bool find_group_item(const int32_t* __restrict__ seg_
 namespace fni8h {
 int launch_quant_rowwise(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, int8_t* q,
                          int64_t ldq, float* s, hipStream_t st);
+// `work` (work_bytes, 256-byte aligned; may be NULL) lets a dense prefill GEMM
+// split K across workgroups.
 int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index,
                 int64_t M, int64_t K, const int8_t* w, const float* ws, int64_t N,
                 int64_t E, const int32_t* seg_off, const uint16_t* bias, uint16_t* y,
-                int64_t ldy, int32_t* acc_out, hipStream_t st);
+                int64_t ldy, int32_t* acc_out, hipStream_t st, int8_t* work = nullptr,
+                int64_t work_bytes = 0);
 // Decode (M <= 4) GEMV with the quantization fused in; returns 1 when the
 // shape is not taken (the caller then quantizes and runs launch_gemm).
 int launch_decode_fused(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const int8_t* w,
@@ -421,10 +424,15 @@ int launch_tile32(const int8_t* aq, int64_t lda, const float* as, const int32_t*
                   const int32_t* seg_off, const uint16_t* bias, uint16_t* y, int64_t ldy,
                   int32_t* acc_out, hipStream_t st);
 // Dense prefill GEMM, two wave groups taking turns at MFMA and memory work
-// (K % 128 == 0); returns 1 when not taken.
+// (K % 128 == 0); returns 1 when not taken.  With a workspace of at least
+// pp_workspace_bytes(M, N, K) bytes it may split K over workgroups.
 int launch_pp(const int8_t* aq, int64_t lda, const float* as, int64_t M, int64_t K,
               const int8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
-              int64_t ldy, int32_t* acc_out, hipStream_t st);
+              int64_t ldy, int32_t* acc_out, int8_t* work, int64_t work_bytes, hipStream_t st);
+int64_t pp_workspace_bytes(int64_t M, int64_t N, int64_t K);
+// Forces the prefill GEMM's tile (bm x bn) and split-K factor where the shape
+// allows it; bm = 0 restores the automatic choice.
+void set_gemm_plan(int64_t bm, int64_t bn, int64_t split);
 int launch_moe_sort(const int32_t* topi, int64_t T, int64_t k, int64_t E, int32_t* seg_off,
                     int32_t* row_token, int32_t* pos, hipStream_t st);
 int launch_moe_combine(const uint16_t* yr, int64_t H, const int32_t* topi,

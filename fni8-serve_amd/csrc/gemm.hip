@@ -451,7 +451,8 @@ namespace fni8h {
 int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* row_index,
                 int64_t M, int64_t K, const int8_t* w, const float* ws, int64_t N,
                 int64_t E, const int32_t* seg_off, const uint16_t* bias, uint16_t* y,
-                int64_t ldy, int32_t* acc_out, hipStream_t st) {
+                int64_t ldy, int32_t* acc_out, hipStream_t st, int8_t* work,
+                int64_t work_bytes) {
     if (M == 0) return FNI8_OK;
     Args a{aq, lda, as, row_index, (int)M, (int)K, w, ws, (int)N, (int)E, seg_off, bias, y,
            ldy, acc_out};
@@ -491,7 +492,7 @@ int launch_gemm(const int8_t* aq, int64_t lda, const float* as, const int32_t* r
             launch_decode(a, st);
         }
     } else {
-        rc = launch_pp(aq, lda, as, M, K, w, ws, N, bias, y, ldy, acc_out, st);
+        rc = launch_pp(aq, lda, as, M, K, w, ws, N, bias, y, ldy, acc_out, work, work_bytes, st);
         if (rc == 1)
             rc = launch_tile32(aq, lda, as, row_index, M, K, w, ws, N, 0, seg_off, bias, y, ldy,
                                acc_out, st);

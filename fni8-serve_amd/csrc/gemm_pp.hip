@@ -34,6 +34,7 @@
 // writes coalesced 16-byte row chunks.
 #include <type_traits>
 
+#include "decode_tile.h"
 #include "tile_common.h"
 
 namespace {
@@ -59,14 +60,62 @@ __device__ __forceinline__ void slot_barrier() {
     __builtin_amdgcn_sched_barrier(0);
 }
 
+// Split-K (SPLIT > 1): the SPLIT workgroups of one output tile each take a
+// contiguous 1/SPLIT of the k-tiles.  Their ids are equal mod 8, so they run on
+// one XCD and hand over through its L2 (the exchange rules of decode_tile.h).
+// Each stores its raw int32 accumulators as a partial tile, waits until the
+// stores are acknowledged, and counts itself in at the tile's counter; the one
+// that arrives last adds the others' partial tiles to its own accumulators and
+// runs the epilogue.  No workgroup waits for another.  A workgroup that peeks
+// at the counter first and finds every other split already in is the last one
+// and skips its own store.  int32 addition is exact, so the output is
+// bit-identical to SPLIT = 1.  The counter holds the low 60 bits of the
+// dispatch's tag and the arrivals in its top 4 bits, so a count left by an
+// earlier launch is never taken up and the workspace needs no clearing (the
+// tag's low bits are the ones that differ between nearby dispatches).  A workgroup that finds
+// itself on another XCD than its tile's (where the L2 exchange cannot work)
+// computes the whole K range and writes the tile alone; the others of its tile
+// then never complete the count, or write the same bits.
+constexpr int kFlagWords = 16;  // u64 words: one counter per 128-byte line
+
+// Workspace of a split plan: the counters (one 128-byte line per tile, rounded
+// up to 256 bytes), then SPLIT partial tiles of BM * BN int32 per tile.
+__host__ __device__ inline int64_t split_flag_bytes(int64_t tiles) {
+    return (tiles * kFlagWords * 8 + 255) & ~(int64_t)255;
+}
+int64_t split_work_bytes(int64_t tiles, int bm, int bn, int split) {
+    if (split <= 1) return 0;
+    return split_flag_bytes(tiles) + tiles * split * (int64_t)bm * bn * 4;
+}
+
+// Tile counter word: arrivals in bits 60..63, the dispatch tag's low 60 bits
+// below them.
+constexpr uint64_t kTagMask = (1ull << 60) - 1;
+constexpr int kCountShift = 60;
+
+// Adds one to the tile counter at p for the dispatch whose tag's low 60 bits
+// are `tag60`; returns the arrivals including this one.  One lane calls it.
+__device__ __forceinline__ int count_in(uint64_t* p, uint64_t tag60) {
+    uint64_t cur = fni8dec::poll_flag(p);
+    for (;;) {
+        const uint64_t nxt = ((cur & kTagMask) == tag60) ? cur + (1ull << kCountShift)
+                                                         : ((1ull << kCountShift) | tag60);
+        uint64_t expect = cur;
+        if (__hip_atomic_compare_exchange_strong(p, &expect, nxt, __ATOMIC_RELAXED,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
+            return (int)(nxt >> kCountShift);
+        cur = expect;
+    }
+}
+
 // WC: waves of a group along N (4: a wave owns BM/2 rows x BN/4 columns; 2: a
 // wave owns BM/4 x BN/2, for BN = 192 where BN/4 is not a multiple of 32).
-template <int BM, int BN, bool WRITE_ACC, int WC = 4>
+template <int BM, int BN, bool WRITE_ACC, int WC = 4, int SPLIT = 1>
 __global__ __launch_bounds__(512) void gemm_pp_kernel(
     const int8_t* __restrict__ aq, int64_t lda, const float* __restrict__ as, int M, int K,
     const int8_t* __restrict__ w, const float* __restrict__ ws, int N,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy,
-    int32_t* __restrict__ acc_out) {
+    int32_t* __restrict__ acc_out, int8_t* __restrict__ work) {
     constexpr int BK = 128, CPR = BK / 16;   // bytes and 16-byte chunks per row per k-tile
     constexpr int STAGE = (BM + BN) * BK;    // bytes per LDS stage (two stages)
     constexpr int D = STAGE / 8192;          // copy instructions per wave per k-tile
@@ -76,6 +125,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     static_assert(WC == 4 || WC == 2, "wave arrangement inside a group");
     static_assert(FM * 64 * WR == BM && FN * 32 * WC == BN, "whole 32x32 blocks per wave");
     static_assert(D * 8192 == STAGE, "a stage must split evenly over the 8 waves");
+    static_assert(SPLIT == 1 || SPLIT == 2 || SPLIT == 4, "split-K factor");
     extern __shared__ __attribute__((aligned(1024))) int8_t smem[];
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -84,9 +134,16 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     const int wrow = g * (BM / 2) + (s / WC) * (FM * 32);  // first row of the wave's blocks
     const int wcol = (s % WC) * (FN * 32);                 // first column
 
+    // workgroup b: split (b / 8) % SPLIT of tile (b / 8 / SPLIT) * 8 + b % 8
+    int tile = blockIdx.x, split = 0;
+    if constexpr (SPLIT > 1) {
+        const int q = tile >> 3;
+        split = q % SPLIT;
+        tile = (q / SPLIT) * 8 + (tile & 7);
+    }
     int m0, m1, n0;
-    fni8t::dense_tile<BM, BN>(M, N, m0, m1, n0);
-    const int KT = K / BK;
+    fni8t::dense_tile_at<BM, BN>(tile, M, N, m0, m1, n0);
+    const int KTS = K / BK / SPLIT;  // k-tiles of one split
     // the epilogue's scales, issued before every copy: the waits for the first
     // k-tile cover them
     const fni8t::TileScales tsc =
@@ -116,15 +173,6 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     const int8_t* abase = aq + (int64_t)m0 * lda;
     const int8_t* bbase = w + (int64_t)n0 * K;
     const uint32_t lds0 = (uint32_t)(uintptr_t)smem;
-    auto issue = [&](int t, int stage) {
-#pragma unroll
-        for (int i = 0; i < D; i++) {
-            const uint32_t l = lds0 + stage * STAGE + (wave * D + i) * 1024;
-            // one instruction, its base chosen by a scalar select (wave-uniform)
-            const bool a_ins = wave * D + i < AINS;
-            copy16_s(l, (a_ins ? abase : bbase) + t * BK, voff[i]);
-        }
-    };
 
     // fragment offsets: lane reads row (lane & 31) of a 32-row block, logical
     // chunk 2q + (lane >> 5) for the 32-byte k step q of the k-tile
@@ -140,70 +188,151 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = i32x16{};
 
-    // prologue: k-tiles 0 and 1 in flight, wait for k-tile 0; group 1 then runs
-    // one slot behind group 0
-    issue(0, 0);
-    if (KT > 1) {
-        issue(1, 1);
-        wait_vmcnt<D>();
-    } else {
-        wait_vmcnt<0>();
-    }
-    slot_barrier();
-    if (g == 1) slot_barrier();
-
-    // Slots: group 0 reads unit u while group 1 computes unit u-1, then group 0
-    // computes unit u while group 1 reads it.  Two 64-byte units per k-tile.
-    // Copy of k-tile t+1 is issued in the first read slot of k-tile t (its stage
-    // last held k-tile t-1, read completely by then); each wave waits for its own
-    // copies of k-tile t+1 before the barrier that precedes group 0's first read
-    // of it (group 1 at the end of its read slot, group 0 after its MFMAs).
-    for (int t0 = 0; t0 < KT; t0 += 2) {
+    // Accumulates k-tiles [tb, tb + nt) into acc.  Starts and ends with every
+    // copy landed and every wave past its last LDS read, so it can run again.
+    auto kloop = [&](int tb, int nt) {
+        const int8_t* ab = abase + (int64_t)tb * BK;
+        const int8_t* bb = bbase + (int64_t)tb * BK;
+        auto issue = [&](int t, int stage) {
 #pragma unroll
-        for (int uu = 0; uu < 4; uu++) {
-            const int t = t0 + (uu >> 1);
-            const int h = uu & 1;
-            const int stage = uu >> 1;
-            const bool live = t < KT;
-            i32x4 af[2][FM], bf[2][FN];
-            if (live) {
-                if (h == 0 && t >= 1 && t + 1 < KT) issue(t + 1, stage ^ 1);
-                const int8_t* sb = smem + stage * STAGE;
-#pragma unroll
-                for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-                    for (int i = 0; i < FM; i++)
-                        af[ks][i] = *reinterpret_cast<const i32x4*>(
-                            sb + (wrow + i * 32) * BK + loff[h * 2 + ks]);
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-                        bf[ks][j] = *reinterpret_cast<const i32x4*>(
-                            sb + BM * BK + (wcol + j * 32) * BK + loff[h * 2 + ks]);
-                }
-                // fragments in registers before the slot ends: once every wave
-                // has passed the barrier the stage may be refilled
-                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-                if (g == 1 && h == 1 && t + 1 < KT) wait_vmcnt<0>();
+            for (int i = 0; i < D; i++) {
+                const uint32_t l = lds0 + stage * STAGE + (wave * D + i) * 1024;
+                // one instruction, its base chosen by a scalar select (wave-uniform)
+                const bool a_ins = wave * D + i < AINS;
+                copy16_s(l, (a_ins ? ab : bb) + t * BK, voff[i]);
             }
-            slot_barrier();
-            if (live) {
-                // the MFMA wave of each SIMD issues ahead of the memory wave
-                __builtin_amdgcn_s_setprio(1);
+        };
+        // prologue: k-tiles 0 and 1 in flight, wait for k-tile 0; group 1 then
+        // runs one slot behind group 0
+        issue(0, 0);
+        if (nt > 1) {
+            issue(1, 1);
+            wait_vmcnt<D>();
+        } else {
+            wait_vmcnt<0>();
+        }
+        slot_barrier();
+        if (g == 1) slot_barrier();
+
+        // Slots: group 0 reads unit u while group 1 computes unit u-1, then group
+        // 0 computes unit u while group 1 reads it.  Two 64-byte units per
+        // k-tile.  Copy of k-tile t+1 is issued in the first read slot of k-tile
+        // t (its stage last held k-tile t-1, read completely by then); each wave
+        // waits for its own copies of k-tile t+1 before the barrier that precedes
+        // group 0's first read of it (group 1 at the end of its read slot, group
+        // 0 after its MFMAs).
+        for (int t0 = 0; t0 < nt; t0 += 2) {
 #pragma unroll
-                for (int ks = 0; ks < 2; ks++)
+            for (int uu = 0; uu < 4; uu++) {
+                const int t = t0 + (uu >> 1);
+                const int h = uu & 1;
+                const int stage = uu >> 1;
+                const bool live = t < nt;
+                i32x4 af[2][FM], bf[2][FN];
+                if (live) {
+                    if (h == 0 && t >= 1 && t + 1 < nt) issue(t + 1, stage ^ 1);
+                    const int8_t* sb = smem + stage * STAGE;
 #pragma unroll
-                    for (int i = 0; i < FM; i++)
+                    for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+                        for (int i = 0; i < FM; i++)
+                            af[ks][i] = *reinterpret_cast<const i32x4*>(
+                                sb + (wrow + i * 32) * BK + loff[h * 2 + ks]);
 #pragma unroll
                         for (int j = 0; j < FN; j++)
-                            acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bf[ks][j], af[ks][i],
-                                                                              acc[i][j], 0, 0, 0);
-                __builtin_amdgcn_s_setprio(0);
-                if (g == 0 && h == 1 && t + 1 < KT) wait_vmcnt<0>();
+                            bf[ks][j] = *reinterpret_cast<const i32x4*>(
+                                sb + BM * BK + (wcol + j * 32) * BK + loff[h * 2 + ks]);
+                    }
+                    // fragments in registers before the slot ends: once every
+                    // wave has passed the barrier the stage may be refilled
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    if (g == 1 && h == 1 && t + 1 < nt) wait_vmcnt<0>();
+                }
+                slot_barrier();
+                if (live) {
+                    // the MFMA wave of each SIMD issues ahead of the memory wave
+                    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+                    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+                        for (int i = 0; i < FM; i++)
+#pragma unroll
+                            for (int j = 0; j < FN; j++)
+                                acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(
+                                    bf[ks][j], af[ks][i], acc[i][j], 0, 0, 0);
+                    __builtin_amdgcn_s_setprio(0);
+                    if (g == 0 && h == 1 && t + 1 < nt) wait_vmcnt<0>();
+                }
+                slot_barrier();
             }
-            slot_barrier();
+        }
+        if (g == 0) slot_barrier();
+    };
+
+    if constexpr (SPLIT == 1) {
+        kloop(0, KTS);
+    } else {
+        constexpr int64_t PART = (int64_t)BM * BN * 4;  // bytes of one partial tile
+        const bool local = fni8dec::xcc_id() == (blockIdx.x & 7u);
+        if (!local) {
+            kloop(0, KTS * SPLIT);  // alone: the whole K range
+        } else {
+            kloop(split * KTS, KTS);
+            const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+            uint64_t* ctr = reinterpret_cast<uint64_t*>(work) + (int64_t)tile * kFlagWords;
+            int8_t* parts = work + split_flag_bytes(tiles) + (int64_t)tile * SPLIT * PART;
+            const uint64_t tag60 = fni8dec::dispatch_tag() & kTagMask;
+            constexpr size_t main_lds = (size_t)2 * (BM + BN) * 128;
+            constexpr size_t word_off =
+                fni8t::tile_scale_offset<BM, BN>(main_lds) + fni8t::tile_scale_lds<BM, BN>();
+            uint32_t* word = reinterpret_cast<uint32_t*>(smem + word_off);  // [2]
+            if (tid == 0) {
+                const uint64_t c = fni8dec::poll_flag(ctr);
+                word[0] = ((c & kTagMask) == tag60 && (int)(c >> kCountShift) == SPLIT - 1) ? 1u : 0u;
+            }
+            __syncthreads();
+            if (__builtin_amdgcn_readfirstlane(word[0]) == 0) {
+                // chunk c = (i*FN + j)*4 + r of every thread: 8 KB contiguous per c
+                uint4* dst = reinterpret_cast<uint4*>(parts + split * PART) + tid;
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            dst[((i * FN + j) * 4 + r) * 512] = make_uint4(
+                                (uint32_t)acc[i][j][4 * r], (uint32_t)acc[i][j][4 * r + 1],
+                                (uint32_t)acc[i][j][4 * r + 2], (uint32_t)acc[i][j][4 * r + 3]);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                __syncthreads();
+                if (tid == 0) word[1] = count_in(ctr, tag60) == SPLIT ? 1u : 0u;
+                __syncthreads();
+                if (__builtin_amdgcn_readfirstlane(word[1]) == 0) return;
+            }
+            // last in: every other split's partial tile is in this XCD's L2
+#pragma unroll 1
+            for (int sp = 0; sp < SPLIT; sp++) {
+                if (sp == split) continue;
+                const uint4* src = reinterpret_cast<const uint4*>(parts + sp * PART) + tid;
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++) {
+                        uint4 v[4];
+#pragma unroll
+                        for (int r = 0; r < 4; r++) v[r] = src[((i * FN + j) * 4 + r) * 512];
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            acc[i][j][4 * r] = (int32_t)((uint32_t)acc[i][j][4 * r] + v[r].x);
+                            acc[i][j][4 * r + 1] = (int32_t)((uint32_t)acc[i][j][4 * r + 1] + v[r].y);
+                            acc[i][j][4 * r + 2] = (int32_t)((uint32_t)acc[i][j][4 * r + 2] + v[r].z);
+                            acc[i][j][4 * r + 3] = (int32_t)((uint32_t)acc[i][j][4 * r + 3] + v[r].w);
+                        }
+                    }
+            }
         }
     }
-    if (g == 0) slot_barrier();
+
     float* sl = reinterpret_cast<float*>(smem + fni8t::tile_scale_offset<BM, BN>(2 * STAGE));
     fni8t::store_tile_scales<BM, BN>(tsc, sl, tid);
     __syncthreads();  // every copy has landed and every wave is done with the stages
@@ -212,20 +341,20 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
                                                     n0, N, bias != nullptr, y, ldy, acc_out);
 }
 
-template <int BM, int BN, int WC = 4>
+template <int BM, int BN, int WC = 4, int SPLIT = 1>
 int launch(const int8_t* aq, int64_t lda, const float* as, int M, int K, const int8_t* w,
            const float* ws, int N, const uint16_t* bias, uint16_t* y, int64_t ldy,
-           int32_t* acc_out, hipStream_t st) {
+           int32_t* acc_out, int8_t* work, hipStream_t st) {
     constexpr size_t main_lds = (size_t)2 * (BM + BN) * 128;
-    constexpr size_t lds =
-        fni8t::tile_scale_offset<BM, BN>(main_lds) + fni8t::tile_scale_lds<BM, BN>();
+    constexpr size_t lds = fni8t::tile_scale_offset<BM, BN>(main_lds) +
+                           fni8t::tile_scale_lds<BM, BN>() + (SPLIT > 1 ? 16 : 0);
     static_assert(lds <= 160 * 1024, "LDS budget");
-    const dim3 grid(((N + BN - 1) / BN) * (unsigned)((M + BM - 1) / BM));
+    const dim3 grid(((N + BN - 1) / BN) * (unsigned)((M + BM - 1) / BM) * SPLIT);
     // The LDS limit is a per-function attribute: each instantiation sets it once
     // (a repeated set with the same value is harmless).
     auto run = [&](auto acc_c) -> int {
         constexpr bool ACC = decltype(acc_c)::value;
-        const auto kern = gemm_pp_kernel<BM, BN, ACC, WC>;
+        const auto kern = gemm_pp_kernel<BM, BN, ACC, WC, SPLIT>;
         static bool attr_set = false;
         if (!attr_set) {
             hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -237,7 +366,7 @@ int launch(const int8_t* aq, int64_t lda, const float* as, int M, int K, const i
             attr_set = true;
         }
         hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, aq, lda, as, M, K, w, ws, N, bias, y,
-                           ldy, acc_out);
+                           ldy, acc_out, work);
         return FNI8_OK;
     };
     if (acc_out) return run(std::true_type{});
@@ -256,14 +385,8 @@ int cu_count() {
     return cus;
 }
 
-}  // namespace
-
-namespace fni8h {
-
-// Returns 1 when the shape is not taken (the caller falls back), else an FNI8 code.
-// Dense only; needs K % 128 == 0 and 16-byte aligned operand rows.  Tiles: the
-// shape from {256x256, 256x192, 128x256, 256x128} with the least estimated
-// time, counting whole rounds of one workgroup per CU and each tile's time
+// ---- tile and split-K choice ---------------------------------------------------
+// Tiles: {256x256, 256x192, 128x256, 256x128}; each tile's time per k-tile
 // relative to 256x256, measured on MI355X over the Qwen3-8B prefill GEMMs:
 // 256x192 takes 0.79 of it for 0.75 of the products (the 2x2 wave arrangement
 // reads 5 fragments per 6 MFMAs instead of 6 per 8), the half-size tiles about
@@ -272,43 +395,137 @@ namespace fni8h {
 // full rounds on 256 CUs where 256x256 leaves the second round half empty
 // (117 -> 103 us).  Between the two half-size tiles, long K (down, K = 12288)
 // runs 256x128 4% faster and short K 128x256 3% faster.
-// Expert segments stay on the 32x32x32 tile kernel: the MoE projections have
-// short K (768 and 2048 bytes, 6 and 16 k-tiles), where a grouped form of this
-// kernel (128x256 segment tiles) measured 18% slower at T = 4096 (473 against
-// 399 us for gate_up + down) -- its pipeline and epilogue are not amortised.
-int launch_pp(const int8_t* aq, int64_t lda, const float* as, int64_t M, int64_t K,
-              const int8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
-              int64_t ldy, int32_t* acc_out, hipStream_t st) {
-    if (K % 128 != 0 || lda % 16 != 0 || ((uintptr_t)aq & 15) || ((uintptr_t)w & 15)) return 1;
-    // per-lane copy offsets are 32-bit: a tile's rows span at most 256 rows
-    if (256 * K >= ((int64_t)1 << 32) || 256 * lda >= ((int64_t)1 << 32)) return 1;
-    const int m = (int)M, k = (int)K, n = (int)N;
+//
+// Split-K (2 or 4) is considered when a workspace is given and the tiles fill
+// less than one round of the CUs: it multiplies the workgroups and divides the
+// k-tiles per workgroup; the hand-over of each partial tile is charged by its
+// size.  Expert segments stay on the 32x32x32 tile kernel: the MoE projections
+// have short K (768 and 2048 bytes, 6 and 16 k-tiles), where a grouped form of
+// this kernel (128x256 segment tiles) measured 18% slower at T = 4096 (473
+// against 399 us for gate_up + down) -- its pipeline and epilogue are not
+// amortised.
+struct PpPlan {
+    int bm, bn, split;
+    int64_t work;  // workspace bytes
+};
+
+constexpr double kPartCost = 1.0;     // per 256x256 partial tile merged, in 256x256 k-tiles
+constexpr double kHandoffCost = 1.0;  // counter and last store latency, same unit
+// k-tiles per split at least: with 16 (K = 4096 split in 2) every split plan
+// measured slower than the best unsplit one on Qwen3-8B's shapes at M = 256..2048
+constexpr int kMinSplitKt = 24;
+
+int g_force_bm = 0, g_force_bn = 0, g_force_split = 0;
+
+bool plan_valid(int64_t M, int64_t N, int64_t K, int bm, int bn, int split, int64_t work_bytes,
+                int64_t& need) {
+    const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    const int64_t kt = K / 128;
+    need = split_work_bytes(tiles, bm, bn, split);
+    if (split == 1) return true;
+    return kt % split == 0 && tiles % 8 == 0 && need <= work_bytes;
+}
+
+// False when the shape is not taken by this kernel.
+bool pp_plan(int64_t M, int64_t N, int64_t K, int64_t work_bytes, PpPlan& out) {
     const int cus = cu_count();
-    const bool longk = K >= 8192;
-    // candidates in order of preference on equal estimates
-    const int kTiles[4][2] = {{256, 256}, {256, 192}, {longk ? 256 : 128, longk ? 128 : 256},
-                              {longk ? 128 : 256, longk ? 256 : 128}};
-    constexpr double kCost[4] = {1.0, 0.79, 0.5 / 0.75, 0.5 / 0.75};  // time of one tile
-    int best = 0;
+    const int fbm = __atomic_load_n(&g_force_bm, __ATOMIC_RELAXED);
+    const int fbn = __atomic_load_n(&g_force_bn, __ATOMIC_RELAXED);
+    const int fsp = __atomic_load_n(&g_force_split, __ATOMIC_RELAXED);
+    int64_t need = 0;
+    if (fbm > 0 && plan_valid(M, N, K, fbm, fbn, fsp, work_bytes, need)) {
+        out = PpPlan{fbm, fbn, fsp, need};
+        return true;
+    }
+    // candidates in order of preference on equal estimates; of the half-size
+    // tiles 256x128 first for long K and for a single row of tiles (M <= 256,
+    // where it reads each weight row once: gate_up at M = 256 45 against 50 us)
+    const bool wide_first = K >= 8192 || M <= 256;
+    const int kTiles[4][2] = {{256, 256}, {256, 192}, {wide_first ? 256 : 128, wide_first ? 128 : 256},
+                              {wide_first ? 128 : 256, wide_first ? 256 : 128}};
+    constexpr double kCost[4] = {1.0, 0.79, 0.5 / 0.75, 0.5 / 0.75};  // per k-tile
+    constexpr int kSplits[3] = {1, 2, 4};
+    const int64_t kt = K / 128;
     double best_t = 1e30;
     int64_t best_wgs = 0;
-    for (int i = 0; i < 4; i++) {
-        const int64_t wgs = ((M + kTiles[i][0] - 1) / kTiles[i][0]) * ((N + kTiles[i][1] - 1) / kTiles[i][1]);
-        const double tm = (double)((wgs + cus - 1) / cus) * kCost[i];
-        if (tm < best_t - 1e-9) {
-            best_t = tm;
-            best = i;
-            best_wgs = wgs;
+    int best_split = 1;
+    for (int sidx = 0; sidx < 3; sidx++) {
+        const int split = kSplits[sidx];
+        for (int i = 0; i < 4; i++) {
+            const int bm = kTiles[i][0], bn = kTiles[i][1];
+            if (split > 1 && bn == 192) continue;
+            if (!plan_valid(M, N, K, bm, bn, split, work_bytes, need)) continue;
+            const int64_t tiles = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+            const int64_t wgs = tiles * split;
+            if (split > 1 && (wgs > cus || kt / split < kMinSplitKt)) continue;
+            double tm = (double)((wgs + cus - 1) / cus) * kCost[i] * (double)(kt / split);
+            if (split > 1)
+                tm += (split - 1) * kPartCost * (double)(bm * bn) / 65536.0 + kHandoffCost;
+            if (tm < best_t - 1e-9) {
+                best_t = tm;
+                best_wgs = wgs;
+                best_split = split;
+                out = PpPlan{bm, bn, split, need};
+            }
         }
     }
-    // Too few workgroups for these tiles (prefill M = 512 except gate_up): the
-    // caller's smaller-tile kernel fills the CUs better.
-    if (4 * best_wgs < 3 * (int64_t)cus) return 1;
-    const int bm = kTiles[best][0], bn = kTiles[best][1];
-    if (bn == 192) return launch<256, 192, 2>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
-    if (bm == 256 && bn == 256) return launch<256, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
-    if (bm == 128) return launch<128, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
-    return launch<256, 128>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, st);
+    // Too few workgroups for unsplit tiles (prefill M = 512 except gate_up):
+    // the caller's smaller-tile kernel fills the CUs better.  Split plans exist
+    // for exactly those shapes and measured faster than it (down at M = 256:
+    // 41 us on 128 workgroups of 256x128 split 4, against 55).
+    return best_split > 1 || 4 * best_wgs >= 3 * (int64_t)cus;
+}
+
+}  // namespace
+
+namespace fni8h {
+
+void set_gemm_plan(int64_t bm, int64_t bn, int64_t split) {
+    const bool ok = (bm == 256 && (bn == 256 || bn == 192 || bn == 128)) || (bm == 128 && bn == 256);
+    const bool sp = split == 1 || ((split == 2 || split == 4) && bn != 192);
+    const bool on = ok && sp;
+    __atomic_store_n(&g_force_split, on ? (int)split : 0, __ATOMIC_RELAXED);
+    __atomic_store_n(&g_force_bn, on ? (int)bn : 0, __ATOMIC_RELAXED);
+    __atomic_store_n(&g_force_bm, on ? (int)bm : 0, __ATOMIC_RELAXED);
+}
+
+bool pp_shape_ok(const int8_t* aq, int64_t lda, int64_t K, const int8_t* w) {
+    if (K % 128 != 0 || lda % 16 != 0 || ((uintptr_t)aq & 15) || ((uintptr_t)w & 15)) return false;
+    // per-lane copy offsets are 32-bit: a tile's rows span at most 256 rows
+    return 256 * K < ((int64_t)1 << 32) && 256 * lda < ((int64_t)1 << 32);
+}
+
+int64_t pp_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M <= 64 || K % 128 != 0 || 256 * K >= ((int64_t)1 << 32)) return 0;
+    PpPlan p;
+    if (!pp_plan(M, N, K, INT64_MAX, p)) return 0;
+    return p.work;
+}
+
+// Returns 1 when the shape is not taken (the caller falls back), else an FNI8 code.
+// Dense only; needs K % 128 == 0 and 16-byte aligned operand rows.
+int launch_pp(const int8_t* aq, int64_t lda, const float* as, int64_t M, int64_t K,
+              const int8_t* w, const float* ws, int64_t N, const uint16_t* bias, uint16_t* y,
+              int64_t ldy, int32_t* acc_out, int8_t* work, int64_t work_bytes, hipStream_t st) {
+    if (!pp_shape_ok(aq, lda, K, w)) return 1;
+    PpPlan p;
+    if (!pp_plan(M, N, K, work != nullptr ? work_bytes : 0, p)) return 1;
+    const int m = (int)M, k = (int)K, n = (int)N;
+    const int bm = p.bm, bn = p.bn;
+    if (p.split == 4) {
+        if (bm == 256 && bn == 256) return launch<256, 256, 4, 4>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
+        if (bm == 128) return launch<128, 256, 4, 4>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
+        return launch<256, 128, 4, 4>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
+    }
+    if (p.split == 2) {
+        if (bm == 256 && bn == 256) return launch<256, 256, 4, 2>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
+        if (bm == 128) return launch<128, 256, 4, 2>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
+        return launch<256, 128, 4, 2>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
+    }
+    if (bn == 192) return launch<256, 192, 2>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, nullptr, st);
+    if (bm == 256 && bn == 256) return launch<256, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, nullptr, st);
+    if (bm == 128) return launch<128, 256>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, nullptr, st);
+    return launch<256, 128>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, nullptr, st);
 }
 
 }  // namespace fni8h

@@ -14,12 +14,13 @@ typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 // XCD-aware order of the dense tiles: consecutive workgroup ids land on
 // different XCDs, so each XCD gets a contiguous band of tiles, walked 8
 // m-tiles at a time.
+// `bid` is the tile's number in launch order (the workgroup id when every
+// workgroup owns one tile).
 template <int BM, int BN>
-__device__ __forceinline__ void dense_tile(int M, int N, int& m0, int& m1, int& n0) {
+__device__ __forceinline__ void dense_tile_at(int bid, int M, int N, int& m0, int& m1, int& n0) {
     const int ntiles_n = (N + BN - 1) / BN;
     const int ntiles_m = (M + BM - 1) / BM;
     const int total = ntiles_m * ntiles_n;
-    int bid = blockIdx.x;
     if ((total & 7) == 0) bid = (bid & 7) * (total >> 3) + (bid >> 3);
     constexpr int GM = 8;
     const int group = bid / (GM * ntiles_n);
@@ -29,6 +30,10 @@ __device__ __forceinline__ void dense_tile(int M, int N, int& m0, int& m1, int& 
     m0 = (first_m + in_group % gsize) * BM;
     m1 = min(M, m0 + BM);
     n0 = (in_group / gsize) * BN;
+}
+template <int BM, int BN>
+__device__ __forceinline__ void dense_tile(int M, int N, int& m0, int& m1, int& n0) {
+    dense_tile_at<BM, BN>(blockIdx.x, M, N, m0, m1, n0);
 }
 
 // ---- epilogue ---------------------------------------------------------------

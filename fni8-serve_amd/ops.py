@@ -143,10 +143,11 @@ def linear_with_intermediates(x: torch.Tensor, qt: QTensor, bias: torch.Tensor |
     if M == 0:
         return y, xq, xs, acc
     # 5..16 tokens on the narrower weights: the one-launch path exchanges the
-    # quantized rows through a workspace.  It comes from the caching allocator like every other buffer:
-    # torch hands a block back to the same stream only, after the work queued
-    # on it, so no two calls that can overlap share one; its contents never
-    # matter, so it is not cleared.
+    # quantized rows through a workspace; prefill shapes with too few output
+    # tiles split K and exchange partial tiles through it.  It comes from the
+    # caching allocator like every other buffer: torch hands a block back to the
+    # same stream only, after the work queued on it, so no two calls that can
+    # overlap share one; its contents never matter, so it is not cleared.
     nw = _lib.workspace_bytes(M, N, K)
     work = torch.empty(nw, dtype=torch.uint8, device=dev) if nw else None
     with torch.cuda.device(dev):
@@ -196,9 +197,12 @@ def gemm_w8a8(xq: torch.Tensor, xs: torch.Tensor, qt: QTensor, bias: torch.Tenso
     acc = torch.empty((M, N), dtype=torch.int32, device=dev) if want_acc else None
     if M:
         ldq = xq.stride(0) if M > 1 else K
+        # split-K workspace for prefill shapes with too few output tiles
+        nw = _lib.workspace_bytes(M, N, K)
+        work = torch.empty(nw, dtype=torch.uint8, device=dev) if nw else None
         with torch.cuda.device(dev):
-            _lib.call("fni8_gemm_w8a8", _ptr(xq), ldq, _ptr(xs), M, K, _ptr(w), _ptr(ws), N,
-                      _ptr(bias), _ptr(y), N, _ptr(acc), _stream(dev))
+            _lib.call("fni8_gemm_w8a8_ws", _ptr(xq), ldq, _ptr(xs), M, K, _ptr(w), _ptr(ws), N,
+                      _ptr(bias), _ptr(y), N, _ptr(acc), _ptr(work), nw, _stream(dev))
     return (y, acc) if want_acc else y
 
 

@@ -93,6 +93,22 @@ int fni8_gemm_w8a8(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, in
                    int64_t ldy, int32_t* acc_out, void* stream);
 
 /*
+ * fni8_gemm_w8a8 with a workspace (replaces the same GEMM half of
+ * fni8serve/layers/linear.py:69 at prefill sizes): the same arithmetic and
+ * outputs, bit for bit.  Where the output has too few 256-wide tiles to fill
+ * the GPU (e.g. Qwen3-8B's down projection, K = 12288, at M = 512 and 2048) the
+ * workgroups of one tile split K between them and hand their int32 partial
+ * tiles over through `workspace`.
+ *   workspace  device memory, 256-byte aligned, at least
+ *              fni8_linear_workspace_bytes(M, N, K) bytes; any contents;
+ *              NULL or too small = no split.  One workspace per stream.
+ */
+int fni8_gemm_w8a8_ws(const int8_t* xq, int64_t ldq, const float* xs, int64_t M, int64_t K,
+                      const int8_t* w, const float* ws, int64_t N, const void* bias, void* y,
+                      int64_t ldy, int32_t* acc_out, void* workspace, int64_t workspace_bytes,
+                      void* stream);
+
+/*
  * The whole W8A8 linear, `fni8.linear(x, qt, bias)` for a per_row_i8 QTensor
  * (replaces fni8serve/layers/linear.py:69): quantize x per token, int8 GEMM
  * against w, dequant epilogue to fp16.
@@ -108,11 +124,12 @@ int fni8_linear_w8a8_f16(const void* x, int64_t ldx, int64_t M, int64_t K, const
 
 /*
  * fni8_linear_w8a8_f16 with a workspace: the same call, arithmetic and
- * outputs (bit for bit), in one launch instead of two where that measured
- * faster -- 5 <= M <= 16 tokens on QKV- and down-shaped weights, 5 <= M <= 8
- * on O-shaped ones (replaces fni8serve/layers/linear.py:69 at decode batch
- * sizes).  The per-token quantization then runs once per XCD and reaches the
- * GEMM workgroups through that XCD's L2; `workspace` holds the exchanged rows.
+ * outputs (bit for bit), faster where the workspace helps (replaces
+ * fni8serve/layers/linear.py:69).  At decode batch sizes -- 5 <= M <= 16 tokens
+ * on QKV- and down-shaped weights, 5 <= M <= 8 on O-shaped ones -- one launch
+ * instead of two: the per-token quantization runs once per XCD and reaches the
+ * GEMM workgroups through that XCD's L2, and `workspace` holds the exchanged
+ * rows.  At prefill sizes the GEMM may split K as fni8_gemm_w8a8_ws does.
  * Other shapes take the same launches as fni8_linear_w8a8_f16.
  *   workspace        device memory, 256-byte aligned, at least
  *                    fni8_linear_workspace_bytes(M, N, K) bytes; any contents
@@ -127,11 +144,16 @@ int fni8_linear_w8a8_f16_ws(const void* x, int64_t ldx, int64_t M, int64_t K, co
                             int64_t workspace_bytes, void* stream);
 
 /*
- * Workspace bytes fni8_linear_w8a8_f16_ws uses for M tokens, N outputs and K
- * inputs: 8 * (2304 + M * K rounded up to 256) where the one-launch path takes
- * the shape (5 <= M <= 16 with 4096 < N < 16384 and K = 4096, or N <= 4096 and
- * K = 12288; 5 <= M <= 8 with N <= 4096 and K = 4096), else 0 (no workspace is
- * used).  At most 8 * (2304 + 16 * 12288) = 1,591,296.
+ * Workspace bytes fni8_linear_w8a8_f16_ws and fni8_gemm_w8a8_ws use for M
+ * tokens, N outputs and K inputs (0: no workspace is used).
+ *   M <= 16: 8 * (2304 + M * K rounded up to 256) where the one-launch path
+ *     takes the shape (5 <= M <= 16 with 4096 < N < 16384 and K = 4096, or
+ *     N <= 4096 and K = 12288; 5 <= M <= 8 with N <= 4096 and K = 4096), at
+ *     most 8 * (2304 + 16 * 12288) = 1,591,296; fni8_gemm_w8a8_ws uses none.
+ *   M > 64: where the prefill GEMM splits K (down-shaped weights, K = 12288,
+ *     below M = 4096), one 128-byte counter per output tile (rounded up to
+ *     256 bytes) plus `split` int32 partial tiles per output tile -- 64 MiB +
+ *     16 KiB for [2048, 12288] x [4096, 12288], 32 MiB + 8 KiB at M = 512.
  */
 int64_t fni8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
@@ -144,6 +166,16 @@ int64_t fni8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
  * which must give the same bits.  Process-wide; affects later launches.
  */
 void fni8_debug_coop_wait_ticks(int64_t ticks);
+
+/*
+ * Test hook, no counterpart in the reference: forces the prefill GEMM's output
+ * tile (bm x bn: 256x256, 256x192, 128x256 or 256x128) and split-K factor
+ * (1, 2 or 4; 1 for 256x192) on every later launch whose shape allows it
+ * (K / 128 a multiple of the split, the tile count a multiple of 8 and a big
+ * enough workspace when split > 1); other values restore the automatic choice.
+ * The output is the same bits under every plan.  Process-wide.
+ */
+void fni8_debug_gemm_plan(int64_t bm, int64_t bn, int64_t split);
 
 /*
  * fni8_linear_w8a8_f16 for callers that cannot allocate (code under HIP graph

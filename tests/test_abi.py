@@ -140,6 +140,48 @@ def test_moe_route_argument_errors(lib):
     assert lib.fni8_moe_route(fake, 1, 128, 128, 0, None, 0, 0, 8, 1, F(1.0), None, fake, None) == -1
 
 
+def test_split_k_workspace_size_and_argument_checks(lib):
+    """The prefill GEMM's split-K workspace: one 128-byte counter line per output
+    tile (rounded up to 256 bytes), then `split` int32 partial tiles per output
+    tile, for the plan the test hook forces; none where the plan cannot split
+    (tile count not a multiple of 8, K / 128 not a multiple of the split) or at
+    decode sizes; a misaligned workspace is an argument error raised before any
+    launch."""
+    def need(M, N, K, bm, bn, split):
+        tiles = -(-M // bm) * -(-N // bn)
+        return ((tiles * 128 + 255) // 256) * 256 + tiles * split * bm * bn * 4
+    try:
+        for (M, N, K, bm, bn, split) in ((2048, 4096, 12288, 256, 256, 2),
+                                         (512, 4096, 12288, 128, 256, 4),
+                                         (500, 1000, 1024, 256, 128, 4),
+                                         (500, 1000, 1024, 256, 256, 2)):
+            lib.fni8_debug_gemm_plan(bm, bn, split)
+            assert lib.fni8_linear_workspace_bytes(M, N, K) == need(M, N, K, bm, bn, split)
+        # 3 x 4 = 12 tiles; 1152 / 128 = 9 k-tiles: the forced plan is not taken
+        lib.fni8_debug_gemm_plan(128, 256, 2)
+        assert lib.fni8_linear_workspace_bytes(300, 1000, 1024) != need(300, 1000, 1024, 128, 256, 2)
+        lib.fni8_debug_gemm_plan(256, 256, 2)
+        assert lib.fni8_linear_workspace_bytes(512, 2048, 1152) == 0
+        lib.fni8_debug_gemm_plan(256, 128, 1)
+        assert lib.fni8_linear_workspace_bytes(2048, 4096, 12288) == 0
+    finally:
+        lib.fni8_debug_gemm_plan(0, 0, 0)
+    for M in (17, 33, 64):
+        assert lib.fni8_linear_workspace_bytes(M, 4096, 12288) == 0
+    assert lib.fni8_linear_workspace_bytes(2048, 4096, 12288) > 0  # down at M = 2048 splits K
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    rc = lib.fni8_gemm_w8a8_ws(fake, 4096, fake, 512, 4096, fake, fake, 64, None, fake, 64, None,
+                               P(0x1080), 1 << 20, None)
+    assert rc == -3 and b"workspace" in lib.fni8_last_error()
+    rc = lib.fni8_gemm_w8a8_ws(fake, 4096, fake, 512, 4096, fake, fake, 64, None, fake, 64, None,
+                               fake, -5, None)
+    assert rc == -3
+    rc = lib.fni8_gemm_w8a8_ws(None, 4096, fake, 512, 4096, fake, fake, 64, None, fake, 64, None,
+                               fake, 1 << 20, None)
+    assert rc == -1
+
+
 def test_workspace_size_and_argument_checks(lib):
     """The one-launch path's workspace: 8 regions of (2304 + M*K rounded up to
     256) bytes for the shapes it takes (5..16 tokens on QKV- and down-shaped
