@@ -273,6 +273,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
         kloop(0, KTS);
     } else {
         constexpr int64_t PART = (int64_t)BM * BN * 4;  // bytes of one partial tile
+        static_assert(FM * FN * 4 * 512 * 16 == PART, "16 bytes per thread per register group");
         const bool local = fni8dec::xcc_id() == (blockIdx.x & 7u);
         if (!local) {
             kloop(0, KTS * SPLIT);  // alone: the whole K range
@@ -386,7 +387,8 @@ int cu_count() {
 }
 
 // ---- tile and split-K choice ---------------------------------------------------
-// Tiles: {256x256, 256x192, 128x256, 256x128}; each tile's time per k-tile
+// Tiles: {256x256, 256x192, 128x256, 256x128}, and 64x128 for long K at
+// M <= 256 (below); each tile's time per k-tile
 // relative to 256x256, measured on MI355X over the Qwen3-8B prefill GEMMs:
 // 256x192 takes 0.79 of it for 0.75 of the products (the 2x2 wave arrangement
 // reads 5 fragments per 6 MFMAs instead of 6 per 8), the half-size tiles about
@@ -437,6 +439,14 @@ bool pp_plan(int64_t M, int64_t N, int64_t K, int64_t work_bytes, PpPlan& out) {
         out = PpPlan{fbm, fbn, fsp, need};
         return true;
     }
+    // Long K on a single row of 256-row tiles (down at M <= 256): 64x128 tiles
+    // split 4, three workgroups per CU (LDS 50 KB each).  Measured at M = 256:
+    // 32.7 us against 41.3 for 256x128 split 4 and 55 on the tile kernel.
+    if (K >= 8192 && M <= 256 && plan_valid(M, N, K, 64, 128, 4, work_bytes, need) &&
+        (K / 128) / 4 >= kMinSplitKt) {
+        out = PpPlan{64, 128, 4, need};
+        return true;
+    }
     // candidates in order of preference on equal estimates; of the half-size
     // tiles 256x128 first for long K and for a single row of tiles (M <= 256,
     // where it reads each weight row once: gate_up at M = 256 45 against 50 us)
@@ -481,7 +491,8 @@ bool pp_plan(int64_t M, int64_t N, int64_t K, int64_t work_bytes, PpPlan& out) {
 namespace fni8h {
 
 void set_gemm_plan(int64_t bm, int64_t bn, int64_t split) {
-    const bool ok = (bm == 256 && (bn == 256 || bn == 192 || bn == 128)) || (bm == 128 && bn == 256);
+    const bool ok = (bm == 256 && (bn == 256 || bn == 192 || bn == 128)) ||
+                    (bm == 128 && bn == 256) || (bm == 64 && bn == 128);
     const bool sp = split == 1 || ((split == 2 || split == 4) && bn != 192);
     const bool on = ok && sp;
     __atomic_store_n(&g_force_split, on ? (int)split : 0, __ATOMIC_RELAXED);
@@ -512,6 +523,11 @@ int launch_pp(const int8_t* aq, int64_t lda, const float* as, int64_t M, int64_t
     if (!pp_plan(M, N, K, work != nullptr ? work_bytes : 0, p)) return 1;
     const int m = (int)M, k = (int)K, n = (int)N;
     const int bm = p.bm, bn = p.bn;
+    if (bm == 64) {  // three workgroups per CU
+        if (p.split == 4) return launch<64, 128, 4, 4>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
+        if (p.split == 2) return launch<64, 128, 4, 2>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
+        return launch<64, 128>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, nullptr, st);
+    }
     if (p.split == 4) {
         if (bm == 256 && bn == 256) return launch<256, 256, 4, 4>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);
         if (bm == 128) return launch<128, 256, 4, 4>(aq, lda, as, m, k, w, ws, n, bias, y, ldy, acc_out, work, st);

@@ -153,7 +153,8 @@ int fni8_linear_w8a8_f16_ws(const void* x, int64_t ldx, int64_t M, int64_t K, co
  *   M > 64: where the prefill GEMM splits K (down-shaped weights, K = 12288,
  *     below M = 4096), one 128-byte counter per output tile (rounded up to
  *     256 bytes) plus `split` int32 partial tiles per output tile -- 64 MiB +
- *     16 KiB for [2048, 12288] x [4096, 12288], 32 MiB + 8 KiB at M = 512.
+ *     16 KiB for [2048, 12288] x [4096, 12288], 32 MiB + 8 KiB at M = 512,
+ *     16 MiB + 16 KiB at M = 256.
  */
 int64_t fni8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
@@ -169,7 +170,7 @@ void fni8_debug_coop_wait_ticks(int64_t ticks);
 
 /*
  * Test hook, no counterpart in the reference: forces the prefill GEMM's output
- * tile (bm x bn: 256x256, 256x192, 128x256 or 256x128) and split-K factor
+ * tile (bm x bn: 256x256, 256x192, 128x256, 256x128 or 64x128) and split-K factor
  * (1, 2 or 4; 1 for 256x192) on every later launch whose shape allows it
  * (K / 128 a multiple of the split, the tile count a multiple of 8 and a big
  * enough workspace when split > 1); other values restore the automatic choice.

@@ -22,7 +22,7 @@ from oracle import oracle
 pytestmark = pytest.mark.gpu
 
 SPLIT_PLANS = [(256, 256, 2), (256, 256, 4), (128, 256, 2), (128, 256, 4), (256, 128, 2),
-               (256, 128, 4)]
+               (256, 128, 4), (64, 128, 2), (64, 128, 4)]
 
 
 def _ptr(t):
@@ -86,7 +86,7 @@ def _inputs(wl, M, N, K, seed):
 
 @pytest.mark.parametrize("bm,bn,split", SPLIT_PLANS)
 def test_split_plans_bitexact_small(lib, plan, wl, cuda, bm, bn, split):
-    """M = 500, N = 1000 (ragged in both, 8 or 16 tiles), K = 1024 (8 k-tiles:
+    """M = 500, N = 1000 (ragged in both, 8 to 64 tiles), K = 1024 (8 k-tiles:
     2 or 4 per split), with bias and accumulators: every output against the
     oracle, every tile counted in, on a workspace of stale bytes."""
     M, N, K = 500, 1000, 1024
