@@ -360,6 +360,73 @@ def prefill_one(pkg, wl, pool, device, name, M, reps=8):
             "gemm_us": round(tg * 1e6, 2), "quant_us": round(tq * 1e6, 2)}
 
 
+def decode_phases_section(pkg, wl, pool, device, ms=(1, 16)):
+    """Where a decode linear's time goes (not in the default sections): per call,
+    best of three sleep-backed bursts over the pool's layers, for each linear at
+    M tokens -- `linear()` as shipped, the two-launch path without a workspace,
+    the GEMM launch alone on already-quantized rows, the quantize launch alone,
+    and (where the one-launch path takes the shape) that launch with every
+    workgroup quantizing for itself."""
+    from importlib import import_module
+    lib = import_module("fni8serve_amd._lib")
+    raw = lib.load()
+
+    def ptr(t):
+        return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+    st = ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+    def burst(fn):
+        best = 1e9
+        for _ in range(3):
+            fn(pool[0])
+            torch.cuda.synchronize()
+            torch.cuda._sleep(int(2.0e7))
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for layer in pool:
+                fn(layer)
+            e1.record()
+            torch.cuda.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / len(pool))
+        return round(best, 2)
+
+    out = {}
+    for name, (N, K) in wl.QWEN3_8B_LINEARS.items():
+        for M in ms:
+            x = wl.activations(M, K, seed=77 + M, device="cpu").to(device)
+            xq, xs = pkg.quantize_rowwise(x)
+            y = torch.empty((M, N), dtype=torch.float16, device=device)
+            q2 = torch.empty((M, K), dtype=torch.int8, device=device)
+            s2 = torch.empty((M,), dtype=torch.float32, device=device)
+
+            def two(L, name=name, x=x, N=N, K=K, M=M):
+                qt = L[name]
+                lib.call("fni8_linear_w8a8_f16", ptr(x), K, M, K, ptr(qt.data), ptr(qt.scale), N,
+                         None, ptr(y), N, ptr(q2), ptr(s2), None, st)
+
+            def gemm(L, name=name, N=N, K=K, M=M):
+                qt = L[name]
+                lib.call("fni8_gemm_w8a8", ptr(xq), K, ptr(xs), M, K, ptr(qt.data), ptr(qt.scale),
+                         N, None, ptr(y), N, None, st)
+
+            k = f"{name}_M{M}"
+            out[f"{k}_linear_us"] = burst(lambda L, name=name, x=x: pkg.linear(x, L[name]))
+            out[f"{k}_two_launch_us"] = burst(two)
+            out[f"{k}_gemm_only_us"] = burst(gemm)
+            out[f"{k}_quant_only_us"] = burst(
+                lambda L, x=x, M=M, K=K: lib.call("fni8_quantize_rowwise_f16", ptr(x), M, K, K,
+                                                  ptr(q2), K, ptr(s2), st))
+            if lib.workspace_bytes(M, N, K):
+                raw.fni8_debug_coop_wait_ticks(0)
+                try:
+                    out[f"{k}_self_quantize_us"] = burst(
+                        lambda L, name=name, x=x: pkg.linear(x, L[name]))
+                finally:
+                    raw.fni8_debug_coop_wait_ticks(-1)
+    return out
+
+
 def vendor_section(pkg, wl, pool, device, ms=(512, 2048, 4096)):
     """The int8 GEMM against the vendor library on the same operands: this
     library's GEMM launch (`gemm_w8a8`, fused dequant epilogue to fp16) and
@@ -974,6 +1041,9 @@ def run_sections(result, sections, pkg, wl, pool, device):
     if "vendor" in sections:
         result["vendor"] = vendor_section(pkg, wl, pool, device)
         log(f"vendor: {result['vendor']}")
+    if "decode_phases" in sections:
+        result["decode_phases"] = decode_phases_section(pkg, wl, pool, device)
+        log(f"decode_phases: {result['decode_phases']}")
     if "fp16_error" in sections:
         result["fp16_error"] = fp16_error_section(pkg, wl, device)
         log(f"fp16_error: {result['fp16_error']}")
