@@ -61,51 +61,34 @@ __device__ __forceinline__ void slot_barrier() {
 }
 
 // Split-K (SPLIT > 1): the SPLIT workgroups of one output tile each take a
-// contiguous 1/SPLIT of the k-tiles.  Their ids are equal mod 8, so they run on
-// one XCD and hand over through its L2 (the exchange rules of decode_tile.h).
-// Each stores its raw int32 accumulators as a partial tile, waits until the
-// stores are acknowledged, and counts itself in at the tile's counter; the one
-// that arrives last adds the others' partial tiles to its own accumulators and
-// runs the epilogue.  No workgroup waits for another.  A workgroup that peeks
-// at the counter first and finds every other split already in is the last one
-// and skips its own store.  int32 addition is exact, so the output is
-// bit-identical to SPLIT = 1.  The counter holds the low 60 bits of the
-// dispatch's tag and the arrivals in its top 4 bits, so a count left by an
-// earlier launch is never taken up and the workspace needs no clearing (the
-// tag's low bits are the ones that differ between nearby dispatches).  A workgroup that finds
-// itself on another XCD than its tile's (where the L2 exchange cannot work)
-// computes the whole K range and writes the tile alone; the others of its tile
-// then never complete the count, or write the same bits.
-constexpr int kFlagWords = 16;  // u64 words: one counter per 128-byte line
+// contiguous 1/SPLIT of the k-tiles.  Their ids are equal mod 8, so with the
+// round-robin dispatch over the 8 XCDs they run on one XCD and hand over
+// through its L2 (the exchange rules of decode_tile.h).  The workgroup of the
+// last split (the highest id of the tile, dispatched last) owns the tile:
+//   * every other split stores its raw int32 accumulators as a partial tile,
+//     waits until the stores are acknowledged by the L2, and publishes a flag
+//     holding the dispatch's tag in the flag region of the XCD it runs on;
+//   * the owner polls its own XCD's flags (L2 atomics, a bounded wait), adds
+//     each partial tile whose flag it sees to its accumulators, recomputes any
+//     other split's k-tiles itself, and runs the epilogue.
+// A flag is only seen by a workgroup on the XCD that wrote it, so a partial
+// tile is only read from the L2 that holds it; where the placement differs
+// from the round-robin one, or a partner runs late, the owner recomputes.  The
+// output is therefore the same bits whatever the placement, and bit-identical
+// to SPLIT = 1 (int32 addition is exact).  A flag left by an earlier launch
+// holds another tag, so the workspace needs no clearing.
+constexpr int kFlagWords = 16;  // u64 words: one flag per 128-byte line
+constexpr int kXcds = 8;
 
-// Workspace of a split plan: the counters (one 128-byte line per tile, rounded
-// up to 256 bytes), then SPLIT partial tiles of BM * BN int32 per tile.
-__host__ __device__ inline int64_t split_flag_bytes(int64_t tiles) {
-    return (tiles * kFlagWords * 8 + 255) & ~(int64_t)255;
+// Workspace of a split plan: the flags (8 XCD regions of tiles * SPLIT lines,
+// rounded up to 256 bytes), then SPLIT - 1 partial tiles of BM * BN int32 per
+// tile.
+__host__ __device__ inline int64_t split_flag_bytes(int64_t tiles, int split) {
+    return (kXcds * tiles * split * kFlagWords * 8 + 255) & ~(int64_t)255;
 }
 int64_t split_work_bytes(int64_t tiles, int bm, int bn, int split) {
     if (split <= 1) return 0;
-    return split_flag_bytes(tiles) + tiles * split * (int64_t)bm * bn * 4;
-}
-
-// Tile counter word: arrivals in bits 60..63, the dispatch tag's low 60 bits
-// below them.
-constexpr uint64_t kTagMask = (1ull << 60) - 1;
-constexpr int kCountShift = 60;
-
-// Adds one to the tile counter at p for the dispatch whose tag's low 60 bits
-// are `tag60`; returns the arrivals including this one.  One lane calls it.
-__device__ __forceinline__ int count_in(uint64_t* p, uint64_t tag60) {
-    uint64_t cur = fni8dec::poll_flag(p);
-    for (;;) {
-        const uint64_t nxt = ((cur & kTagMask) == tag60) ? cur + (1ull << kCountShift)
-                                                         : ((1ull << kCountShift) | tag60);
-        uint64_t expect = cur;
-        if (__hip_atomic_compare_exchange_strong(p, &expect, nxt, __ATOMIC_RELAXED,
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))
-            return (int)(nxt >> kCountShift);
-        cur = expect;
-    }
+    return split_flag_bytes(tiles, split) + tiles * (split - 1) * (int64_t)bm * bn * 4;
 }
 
 // WC: waves of a group along N (4: a wave owns BM/2 rows x BN/4 columns; 2: a
@@ -115,7 +98,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     const int8_t* __restrict__ aq, int64_t lda, const float* __restrict__ as, int M, int K,
     const int8_t* __restrict__ w, const float* __restrict__ ws, int N,
     const uint16_t* __restrict__ bias, uint16_t* __restrict__ y, int64_t ldy,
-    int32_t* __restrict__ acc_out, int8_t* __restrict__ work) {
+    int32_t* __restrict__ acc_out, int8_t* __restrict__ work, uint64_t wait_ticks) {
     constexpr int BK = 128, CPR = BK / 16;   // bytes and 16-byte chunks per row per k-tile
     constexpr int STAGE = (BM + BN) * BK;    // bytes per LDS stage (two stages)
     constexpr int D = STAGE / 8192;          // copy instructions per wave per k-tile
@@ -199,7 +182,7 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
                 const uint32_t l = lds0 + stage * STAGE + (wave * D + i) * 1024;
                 // one instruction, its base chosen by a scalar select (wave-uniform)
                 const bool a_ins = wave * D + i < AINS;
-                copy16_s(l, (a_ins ? ab : bb) + t * BK, voff[i]);
+                copy16_s(l, (a_ins ? ab : bb) + (int64_t)t * BK, voff[i]);
             }
         };
         // prologue: k-tiles 0 and 1 in flight, wait for k-tile 0; group 1 then
@@ -274,46 +257,71 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
     } else {
         constexpr int64_t PART = (int64_t)BM * BN * 4;  // bytes of one partial tile
         static_assert(FM * FN * 4 * 512 * 16 == PART, "16 bytes per thread per register group");
-        const bool local = fni8dec::xcc_id() == (blockIdx.x & 7u);
-        if (!local) {
-            kloop(0, KTS * SPLIT);  // alone: the whole K range
-        } else {
-            kloop(split * KTS, KTS);
-            const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
-            uint64_t* ctr = reinterpret_cast<uint64_t*>(work) + (int64_t)tile * kFlagWords;
-            int8_t* parts = work + split_flag_bytes(tiles) + (int64_t)tile * SPLIT * PART;
-            const uint64_t tag60 = fni8dec::dispatch_tag() & kTagMask;
-            constexpr size_t main_lds = (size_t)2 * (BM + BN) * 128;
-            constexpr size_t word_off =
-                fni8t::tile_scale_offset<BM, BN>(main_lds) + fni8t::tile_scale_lds<BM, BN>();
-            uint32_t* word = reinterpret_cast<uint32_t*>(smem + word_off);  // [2]
-            if (tid == 0) {
-                const uint64_t c = fni8dec::poll_flag(ctr);
-                word[0] = ((c & kTagMask) == tag60 && (int)(c >> kCountShift) == SPLIT - 1) ? 1u : 0u;
+        const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+        const uint32_t xcc = fni8dec::xcc_id();
+        // this XCD's flags of the tile: [SPLIT] lines
+        uint64_t* flags = reinterpret_cast<uint64_t*>(work) +
+                          (((int64_t)xcc * tiles + tile) * SPLIT) * kFlagWords;
+        int8_t* parts = work + split_flag_bytes(tiles, SPLIT) + (int64_t)tile * (SPLIT - 1) * PART;
+        const uint64_t tag = fni8dec::dispatch_tag();
+        constexpr size_t main_lds = (size_t)2 * (BM + BN) * 128;
+        constexpr size_t word_off =
+            fni8t::tile_scale_offset<BM, BN>(main_lds) + fni8t::tile_scale_lds<BM, BN>();
+        uint32_t* ready = reinterpret_cast<uint32_t*>(smem + word_off);
+        // One call site of the main loop: its own split's k-tiles, and for the
+        // owner, if some partner's tile does not arrive within the wait bound,
+        // the whole K range once more from zero.
+        int tb = split * KTS, nt = KTS;
+        bool merge = false;
+        for (int pass = 0;; pass++) {
+            kloop(tb, nt);
+            if (split != SPLIT - 1 || pass > 0) break;
+            if (wave == 0) {
+                bool ok = true;
+                for (int sp = 0; sp < SPLIT - 1 && ok; sp++) {
+                    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+                    for (;;) {
+                        uint64_t f = tag;
+                        if (lane == 0) f = fni8dec::poll_flag(flags + sp * kFlagWords);
+                        ok = __ballot(f != tag) == 0;
+                        if (ok || __builtin_amdgcn_s_memrealtime() - t0 >= wait_ticks) break;
+                        __builtin_amdgcn_s_sleep(2);
+                    }
+                }
+                if (lane == 0) ready[0] = ok ? 1u : 0u;
             }
             __syncthreads();
-            if (__builtin_amdgcn_readfirstlane(word[0]) == 0) {
-                // chunk c = (i*FN + j)*4 + r of every thread: 8 KB contiguous per c
-                uint4* dst = reinterpret_cast<uint4*>(parts + split * PART) + tid;
-#pragma unroll
-                for (int i = 0; i < FM; i++)
-#pragma unroll
-                    for (int j = 0; j < FN; j++)
-#pragma unroll
-                        for (int r = 0; r < 4; r++)
-                            dst[((i * FN + j) * 4 + r) * 512] = make_uint4(
-                                (uint32_t)acc[i][j][4 * r], (uint32_t)acc[i][j][4 * r + 1],
-                                (uint32_t)acc[i][j][4 * r + 2], (uint32_t)acc[i][j][4 * r + 3]);
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-                __syncthreads();
-                if (tid == 0) word[1] = count_in(ctr, tag60) == SPLIT ? 1u : 0u;
-                __syncthreads();
-                if (__builtin_amdgcn_readfirstlane(word[1]) == 0) return;
+            if (__builtin_amdgcn_readfirstlane(ready[0]) != 0) {
+                merge = true;
+                break;
             }
-            // last in: every other split's partial tile is in this XCD's L2
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) acc[i][j] = i32x16{};
+            tb = 0;
+            nt = KTS * SPLIT;
+        }
+        if (split != SPLIT - 1) {
+            // chunk c = (i*FN + j)*4 + r of every thread: 8 KB contiguous per c
+            uint4* dst = reinterpret_cast<uint4*>(parts + split * PART) + tid;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++)
+                        dst[((i * FN + j) * 4 + r) * 512] =
+                            make_uint4((uint32_t)acc[i][j][4 * r], (uint32_t)acc[i][j][4 * r + 1],
+                                       (uint32_t)acc[i][j][4 * r + 2], (uint32_t)acc[i][j][4 * r + 3]);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0) fni8dec::publish_flag(flags + split * kFlagWords, tag);
+            return;
+        }
+        if (merge) {
 #pragma unroll 1
-            for (int sp = 0; sp < SPLIT; sp++) {
-                if (sp == split) continue;
+            for (int sp = 0; sp < SPLIT - 1; sp++) {
                 const uint4* src = reinterpret_cast<const uint4*>(parts + sp * PART) + tid;
 #pragma unroll
                 for (int i = 0; i < FM; i++)
@@ -332,6 +340,9 @@ __global__ __launch_bounds__(512) void gemm_pp_kernel(
                     }
             }
         }
+        // test visibility: the owner's own flag line in this XCD's region records
+        // whether it merged its partners' tiles (1) or recomputed the tile (0)
+        if (tid == 0) flags[(SPLIT - 1) * kFlagWords] = merge ? 1ull : 0ull;
     }
 
     float* sl = reinterpret_cast<float*>(smem + fni8t::tile_scale_offset<BM, BN>(2 * STAGE));
@@ -351,6 +362,7 @@ int launch(const int8_t* aq, int64_t lda, const float* as, int M, int K, const i
                            fni8t::tile_scale_lds<BM, BN>() + (SPLIT > 1 ? 16 : 0);
     static_assert(lds <= 160 * 1024, "LDS budget");
     const dim3 grid(((N + BN - 1) / BN) * (unsigned)((M + BM - 1) / BM) * SPLIT);
+    const uint64_t wait_ticks = SPLIT > 1 ? fni8h::xcd_wait_ticks() : 0;
     // The LDS limit is a per-function attribute: each instantiation sets it once
     // (a repeated set with the same value is harmless).
     auto run = [&](auto acc_c) -> int {
@@ -367,7 +379,7 @@ int launch(const int8_t* aq, int64_t lda, const float* as, int M, int K, const i
             attr_set = true;
         }
         hipLaunchKernelGGL(kern, grid, dim3(512), lds, st, aq, lda, as, M, K, w, ws, N, bias, y,
-                           ldy, acc_out, work);
+                           ldy, acc_out, work, wait_ticks);
         return FNI8_OK;
     };
     if (acc_out) return run(std::true_type{});

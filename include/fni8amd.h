@@ -151,20 +151,23 @@ int fni8_linear_w8a8_f16_ws(const void* x, int64_t ldx, int64_t M, int64_t K, co
  *     N <= 4096 and K = 12288; 5 <= M <= 8 with N <= 4096 and K = 4096), at
  *     most 8 * (2304 + 16 * 12288) = 1,591,296; fni8_gemm_w8a8_ws uses none.
  *   M > 64: where the prefill GEMM splits K (down-shaped weights, K = 12288,
- *     below M = 4096), one 128-byte counter per output tile (rounded up to
- *     256 bytes) plus `split` int32 partial tiles per output tile -- 64 MiB +
- *     16 KiB for [2048, 12288] x [4096, 12288], 32 MiB + 8 KiB at M = 512,
- *     16 MiB + 16 KiB at M = 256.
+ *     below M = 4096), 8 regions of one 128-byte flag per output tile and
+ *     split (rounded up to 256 bytes) plus `split` - 1 int32 partial tiles per
+ *     output tile -- 32 MiB + 256 KiB for [2048, 12288] x [4096, 12288],
+ *     24 MiB + 256 KiB at M = 512, 12 MiB + 512 KiB at M = 256.
  */
 int64_t fni8_linear_workspace_bytes(int64_t M, int64_t N, int64_t K);
 
 /*
  * Test hook, no counterpart in the reference: the bound, in ticks of the
- * 100 MHz real-time counter, on how long a GEMM workgroup of the one-launch
- * path waits for its XCD's quantized rows before quantizing them itself
- * (default 10000 = 100 us; a negative value restores it).  0 makes every
- * workgroup that does not find the rows at its first look take the fallback,
- * which must give the same bits.  Process-wide; affects later launches.
+ * 100 MHz real-time counter, on the two waits for data handed over inside one
+ * XCD -- a GEMM workgroup of the one-launch decode path waiting for its XCD's
+ * quantized rows (it then quantizes them itself), and the owner of a split-K
+ * prefill tile waiting for its partners' partial tiles (it then recomputes the
+ * tile over the whole K range).  Default 10000 = 100 us; a negative value
+ * restores it.  0 makes every wait that does not succeed at its first look take
+ * the fallback, which must give the same bits.  Process-wide; affects later
+ * launches.
  */
 void fni8_debug_coop_wait_ticks(int64_t ticks);
 

@@ -141,15 +141,16 @@ def test_moe_route_argument_errors(lib):
 
 
 def test_split_k_workspace_size_and_argument_checks(lib):
-    """The prefill GEMM's split-K workspace: one 128-byte counter line per output
-    tile (rounded up to 256 bytes), then `split` int32 partial tiles per output
-    tile, for the plan the test hook forces; none where the plan cannot split
+    """The prefill GEMM's split-K workspace: 8 XCD regions of one 128-byte flag
+    line per output tile and split (rounded up to 256 bytes), then `split` - 1
+    int32 partial tiles per output tile, for the plan the test hook forces; none
+    where the plan cannot split
     (tile count not a multiple of 8, K / 128 not a multiple of the split) or at
     decode sizes; a misaligned workspace is an argument error raised before any
     launch."""
     def need(M, N, K, bm, bn, split):
         tiles = -(-M // bm) * -(-N // bn)
-        return ((tiles * 128 + 255) // 256) * 256 + tiles * split * bm * bn * 4
+        return ((8 * tiles * split * 128 + 255) // 256) * 256 + tiles * (split - 1) * bm * bn * 4
     try:
         for (M, N, K, bm, bn, split) in ((2048, 4096, 12288, 256, 256, 2),
                                          (512, 4096, 12288, 128, 256, 4),

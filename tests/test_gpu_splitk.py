@@ -1,16 +1,19 @@
 """GPU parity of the prefill GEMM with K split over 2 or 4 workgroups per output
-tile (fni8_gemm_w8a8_ws, and fni8_linear_w8a8_f16_ws at prefill sizes): each
-split's int32 partial tile is handed over through the workspace and the
-workgroup that counts in last adds them up and runs the epilogue.
+tile (fni8_gemm_w8a8_ws, and fni8_linear_w8a8_f16_ws at prefill sizes): the
+workgroups of the first splits hand their int32 partial tiles over through the
+workspace, and the tile's owner (the last split) adds them up -- or, if one
+does not arrive within the wait bound, recomputes the whole tile -- and runs the
+epilogue.
 
 Bar: bit-identical int32 accumulators and fp16 outputs against the CPU oracle
 (every output at the small ragged shape, sampled rows at Qwen3-8B's), and
-against the unsplit GEMM on the same inputs under every tile and split.  The
-workspace needs no clearing, so the tests fill it with stale counters and
-garbage first, reuse it across calls, and replay a captured graph on new
-inputs.  After each split call, every tile's counter holds SPLIT - 1 or SPLIT
-arrivals: the proof that the split kernel ran and that its hand-over stayed
-inside one XCD."""
+against the unsplit GEMM on the same inputs under every tile and split, on both
+of the owner's paths (merged, and recomputed with the wait bound forced to 0).
+The workspace needs no clearing, so the tests fill it with garbage first, reuse
+it across calls, and replay a captured graph on new inputs.  On a zeroed
+workspace each tile's owner leaves a merge mark in the flag region of its XCD:
+exactly one mark per tile proves that the split kernel ran and that the
+hand-over took the merge path."""
 import ctypes
 
 import numpy as np
@@ -65,10 +68,11 @@ def _tiles(M, N, bm, bn):
     return -(-M // bm) * -(-N // bn)
 
 
-def _counts(work, tiles):
-    """Arrival count of each tile's counter (one 128-byte line per tile)."""
-    c = work[:tiles * 128].view(torch.int64).view(tiles, 16)[:, 0].cpu().numpy()
-    return (c.view(np.uint64) >> np.uint64(60)).astype(np.int64)
+def _merge_marks(work, tiles, split):
+    """Per tile, the owner's merge marks summed over the 8 XCD flag regions
+    (region x, tile t, split s: 128-byte line (x*tiles + t)*split + s)."""
+    f = work[:8 * tiles * split * 128].view(torch.int64).view(8, tiles, split, 16)
+    return f[:, :, split - 1, 0].sum(dim=0).cpu().numpy()
 
 
 def _stale(nbytes, seed, dev):
@@ -88,25 +92,35 @@ def _inputs(wl, M, N, K, seed):
 def test_split_plans_bitexact_small(lib, plan, wl, cuda, bm, bn, split):
     """M = 500, N = 1000 (ragged in both, 8 to 64 tiles), K = 1024 (8 k-tiles:
     2 or 4 per split), with bias and accumulators: every output against the
-    oracle, every tile counted in, on a workspace of stale bytes."""
+    oracle, on a zeroed workspace (one merge mark per tile), then on a workspace
+    of stale bytes, then with the wait bound at 0 (owners recompute)."""
     M, N, K = 500, 1000, 1024
     xq, xs, q, s = _inputs(wl, M, N, K, seed=1100 + 10 * split + bm // 128)
     bias = (torch.randn(N, generator=torch.Generator().manual_seed(5)) * 3).half()
     plan(bm, bn, split)
     nw = lib.workspace_bytes(M, N, K)
     tiles = _tiles(M, N, bm, bn)
-    assert nw >= tiles * split * bm * bn * 4, f"plan {bm}x{bn}/{split} not taken (workspace {nw})"
-    work = _stale(nw, 7, cuda)
-    y, a = _gemm(lib, torch.from_numpy(xq).to(cuda), torch.from_numpy(xs).to(cuda), q.to(cuda),
-                 s.to(cuda), bias.to(cuda), work, acc=True)
-    torch.cuda.synchronize()
+    assert nw >= tiles * (split - 1) * bm * bn * 4, f"plan {bm}x{bn}/{split} not taken ({nw} B)"
     accr = oracle.gemm_i8(xq, q.numpy())
-    assert np.array_equal(a.cpu().numpy(), accr), "int32 accumulators differ"
     yr = oracle.dequant_f16(accr, xs, s.numpy(), bias.numpy())
-    assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), yr.view(np.uint16)), \
-        "fp16 outputs differ"
-    cnt = _counts(work, tiles)
-    assert np.all((cnt == split - 1) | (cnt == split)), f"tile counters {cnt}"
+    raw = lib.load()
+    for case in ("zeroed", "stale", "recompute"):
+        work = torch.zeros(nw, dtype=torch.uint8, device=cuda) if case == "zeroed" \
+            else _stale(nw, 7, cuda)
+        if case == "recompute":
+            raw.fni8_debug_coop_wait_ticks(0)
+        try:
+            y, a = _gemm(lib, torch.from_numpy(xq).to(cuda), torch.from_numpy(xs).to(cuda),
+                         q.to(cuda), s.to(cuda), bias.to(cuda), work, acc=True)
+            torch.cuda.synchronize()
+        finally:
+            raw.fni8_debug_coop_wait_ticks(-1)
+        assert np.array_equal(a.cpu().numpy(), accr), f"{case}: int32 accumulators differ"
+        assert np.array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16),
+                              yr.view(np.uint16)), f"{case}: fp16 outputs differ"
+        if case == "zeroed":
+            marks = _merge_marks(work, tiles, split)
+            assert np.all(marks == 1), f"merge marks per tile {marks}"
 
 
 @pytest.mark.parametrize("bm,bn,split", SPLIT_PLANS)
@@ -204,7 +218,7 @@ def test_workspace_too_small_falls_back(lib, plan, wl, cuda):
     nw = lib.workspace_bytes(M, N, K)
     assert nw > 0
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    for size in (nw - 1, 1 << 20):   # the smallest split plan here needs 4 MiB
+    for size in (nw - 1, 1 << 20):   # the smallest split plan here needs 2 MiB
         work = torch.zeros(nw, dtype=torch.uint8, device=cuda)
         y = torch.empty((M, N), dtype=torch.float16, device=cuda)
         lib.call("fni8_gemm_w8a8_ws", _ptr(xqd), K, _ptr(xsd), M, K, _ptr(qd), _ptr(sd), N, None,
