@@ -205,6 +205,32 @@ def test_qwen3_shapes_automatic_plan(lib, pkg, wl, cuda, name, M):
                           yr.view(np.uint16))
 
 
+def test_linear_split_k_strided_bias_3d(pkg, wl, cuda):
+    """`linear()` on down-shaped weights at prefill sizes, the split-K plan taken
+    through the workspace: a [B, S, K] input whose rows are a strided view (every
+    other token of a longer sequence), with bias.  Every output against the
+    oracle; the same call on a contiguous copy gives the same bits."""
+    N, K = wl.QWEN3_8B_LINEARS["down"]
+    B, S = 2, 160          # M = 320 rows: the 64x128 / 256x128 split plans' range
+    h = wl.activations(B * 2 * S, K, seed=1600).reshape(B, 2 * S, K)
+    q, s = wl.weight_i8(N, K, seed=1601)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(1602)) * 2).half()
+    qt = pkg.QTensor(q.cuda(), s.cuda(), scheme="per_row_i8")
+    hs = h.cuda()[:, ::2]                      # [B, S, K], token stride 2K
+    assert not hs.is_contiguous()
+    from importlib import import_module
+    assert import_module("fni8serve_amd._lib").workspace_bytes(B * S, N, K) > 0
+    y = pkg.linear(hs, qt, bias.cuda())
+    yc = pkg.linear(hs.contiguous(), qt, bias.cuda())
+    torch.cuda.synchronize()
+    assert y.shape == (B, S, N)
+    assert torch.equal(y.view(torch.int16), yc.view(torch.int16))
+    yr, *_ = oracle.linear_w8a8_f16(h[:, ::2].reshape(-1, K).contiguous().numpy(), q.numpy(),
+                                    s.numpy(), bias.numpy())
+    assert np.array_equal(y.reshape(-1, N).cpu().view(torch.int16).numpy().view(np.uint16),
+                          yr.view(np.uint16))
+
+
 def test_workspace_too_small_falls_back(lib, plan, wl, cuda):
     """A workspace one byte short of the forced plan's: another plan runs (same
     bits).  A workspace smaller than every split plan's: the unsplit GEMM runs
