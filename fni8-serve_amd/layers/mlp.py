@@ -20,11 +20,12 @@ from .activation import SiluAndMul, fused_act, get_act_and_mul
 from .linear import LinearW8A8
 
 # Rows from which the fused activation + quantization feeds the down projection.
-# Below it the unfused chain is faster: one row's activation (12288 exps for
-# Qwen3-8B) runs on a single workgroup in the fused kernel, while the decode
-# GEMV quantizes its input at almost no cost (MI355X, Qwen3-8B down: 10.4 us
-# unfused vs 12.4 us fused at 1 row; fused 1.01-1.07x faster from 4 rows up).
-FUSE_MIN_ROWS = 4
+# Below it the unfused chain is faster: up to 4 rows the down projection's
+# linear() quantizes its own input inside the GEMM at almost no cost, while the
+# fused kernel runs each row's activation (12288 exps for Qwen3-8B) on one
+# workgroup (MI355X, Qwen3-8B down chain, unfused vs fused: 10.07 vs 11.66 us at
+# 1 row, 12.54 vs 14.69 at 4; 15.81 vs 15.50 at 16, 26.73 vs 26.09 at 64).
+FUSE_MIN_ROWS = 5
 
 
 class GatedMLP(nn.Module):

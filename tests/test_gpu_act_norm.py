@@ -271,11 +271,12 @@ def test_fused_kernels_graph_replay(pkg):
 
 
 @pytest.mark.parametrize("act", ["silu", "gelu_tanh"])
-@pytest.mark.parametrize("M", [1, 4, 16, 64, 512])
+@pytest.mark.parametrize("M", [1, 4, 5, 16, 64, 512])
 def test_gated_mlp_fused_equals_unfused(pkg, act, M):
     """GatedMLP on the GPU (gate_up linear -> act_and_mul_quant -> int8 GEMM
-    from 4 rows up) equals the unfused chain down_proj(act_fn(gate_up_proj(x)))
-    bit for bit at Qwen3-8B's MLP shapes; the fused chain itself too at 1 row."""
+    from 5 rows up) equals the unfused chain down_proj(act_fn(gate_up_proj(x)))
+    bit for bit at Qwen3-8B's MLP shapes; the fused chain itself too at 1 and 4
+    rows, where GatedMLP takes the unfused one."""
     print(f"gated mlp {act} M={M}", flush=True)
     from importlib import import_module
     wl = import_module("fni8serve_amd.workloads")
