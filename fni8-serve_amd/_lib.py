@@ -40,11 +40,13 @@ SIGNATURES = {
     "fni8_moe_route": [_P, _I, _I, _I, _C, _P, _I, _I, _I, _C, _F, _P, _P, _P],
     "fni8_act_and_mul_f16": [_P, _I, _I, _I, _C, _P, _I, _P],
     "fni8_act_and_mul_quant_f16": [_P, _I, _I, _I, _C, _P, _I, _P, _P],
+    "fni8_act_and_mul_quant_f16_ws": [_P, _I, _I, _I, _C, _P, _I, _P, _P, _I, _P],
     "fni8_rmsnorm_f16": [_P, _I, _P, _I, _P, _F, _C, _I, _I, _P, _I, _P, _I, _P],
     "fni8_rmsnorm_quant_f16": [_P, _I, _P, _I, _P, _F, _C, _I, _I, _P, _I, _P, _P, _I, _P],
 }
 STRING_FUNCS = ("fni8_strerror", "fni8_last_error", "fni8_version")
-INT64_FUNCS = {"fni8_linear_workspace_bytes": [_I, _I, _I]}
+INT64_FUNCS = {"fni8_linear_workspace_bytes": [_I, _I, _I],
+               "fni8_act_and_mul_quant_workspace_bytes": [_I, _I]}
 VOID_FUNCS = {"fni8_debug_coop_wait_ticks": [_I], "fni8_debug_gemm_plan": [_I, _I, _I]}
 
 _lib = None

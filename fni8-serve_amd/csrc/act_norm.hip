@@ -19,7 +19,7 @@
 // -ffp-contract=off and correctly rounded division and square root), and the
 // sum of squares has a fixed order (below), so a CPU restatement of the same
 // operations reproduces every output bit.
-#include "common.h"
+#include "decode_tile.h"
 
 namespace {
 
@@ -149,6 +149,103 @@ __global__ __launch_bounds__(TPB) void act_quant_vec_kernel(
     for (int c = 0; c < CH; c++) {
         const int k = (c * TPB + tid) * 8;
         if (k < I) *reinterpret_cast<uint2*>(qr + k) = fni8::quant_chunk(a[c], sc, yr, live);
+    }
+}
+
+// act_and_mul + quantization for few rows (16-byte chunks): a row's
+// activations are VALU work (an exp and a division per element), too much for
+// the one workgroup per row above when there are fewer rows than CUs.  So G
+// workgroups share a row, each activating 1/G of its chunks in registers, and
+// the row maximum is assembled from their partial maxima, exchanged through the
+// L2 of the XCD they run on (the exchange rules of decode_tile.h): workgroup b
+// takes part (b/8) % G of row (b/8/G)*8 + b%8, so the G parts of a row have
+// ids equal mod 8 and share an XCD under the round-robin dispatch.  Each part
+// stores its maximum and then a flag holding the dispatch tag into its XCD's
+// region of the workspace, and polls the other parts' flags there (bounded);
+// a part whose flag does not arrive in time is recomputed (its maximum only),
+// so the result is the same bits whatever the placement.
+// Workspace: [8 XCDs][rows rounded up to 8][G] 128-byte lines (flag, maximum).
+constexpr int kSplitLine = 16;  // u64 words per line
+
+template <int ACT, int CH>
+__global__ __launch_bounds__(kThreads) void act_quant_split_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, int M, int I, int G, int8_t* __restrict__ q,
+    int64_t ldq, float* __restrict__ s, uint64_t* __restrict__ work, uint64_t wait_ticks) {
+    __shared__ uint32_t red[kThreads / 64];
+    __shared__ uint32_t found[2];  // [0] max over the parts received, [1] bit mask of missing parts
+    const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63;
+    const int wave = tid >> 6;
+    const int qd = b >> 3, part = qd % G, row = (qd / G) * 8 + (b & 7);
+    if (row >= M) return;
+    const int cpr = I / 8;                 // 16-byte chunks of the row
+    const int per = (cpr + G - 1) / G;     // chunks of a part (<= CH * kThreads)
+    const uint16_t* xr = x + (int64_t)row * ldx;
+    auto part_chunks = [&](int p, uint4 (&a)[CH], bool keep) -> uint32_t {
+        const int c0 = p * per, c1 = min(cpr, c0 + per);
+        uint32_t m = 0;
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const int c = c0 + j * kThreads + tid;
+            if (c < c1) {
+                const uint4 g = *reinterpret_cast<const uint4*>(xr + 8 * c);
+                const uint4 u = *reinterpret_cast<const uint4*>(xr + I + 8 * c);
+                const uint4 v = act_chunk<ACT>(g, u);
+                m = chunk_amax(v, m);
+                if (keep) a[j] = v;
+            }
+        }
+        return m;
+    };
+    uint4 a[CH];
+    uint32_t amax = block_amax(part_chunks(part, a, true), red);
+
+    const int mpad = (M + 7) & ~7;
+    uint64_t* lines = work + ((int64_t)fni8dec::xcc_id() * mpad + row) * G * kSplitLine;
+    const uint64_t tag = fni8dec::dispatch_tag();
+    if (tid == 0) {
+        lines[part * kSplitLine + 1] = amax;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        fni8dec::publish_flag(lines + part * kSplitLine, tag);
+    }
+    // wave 0: lane p waits for part p's flag, then reads its maximum
+    if (wave == 0) {
+        const bool mine = lane < G && lane != part;
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+        bool seen = !mine;
+        for (;;) {
+            if (!seen) seen = fni8dec::poll_flag(lines + lane * kSplitLine) == tag;
+            if (__ballot(!seen) == 0 || __builtin_amdgcn_s_memrealtime() - t0 >= wait_ticks) break;
+            __builtin_amdgcn_s_sleep(2);
+        }
+        uint32_t m = 0;
+        if (mine && seen) m = (uint32_t)fni8dec::poll_flag(lines + lane * kSplitLine + 1);
+        m = fni8::wave_max_uniform(m);
+        const uint64_t miss = __ballot(mine && !seen);
+        if (lane == 0) {
+            found[0] = m;
+            found[1] = (uint32_t)miss;
+        }
+    }
+    __syncthreads();
+    amax = found[0] > amax ? found[0] : amax;
+    const uint32_t miss = __builtin_amdgcn_readfirstlane(found[1]);
+    for (int p = 0; p < G; p++) {
+        if (!((miss >> p) & 1u)) continue;
+        __syncthreads();  // red is reused
+        uint4 tmp[CH];
+        const uint32_t mp = block_amax(part_chunks(p, tmp, false), red);
+        amax = mp > amax ? mp : amax;
+    }
+    const float sc = fni8::row_scale_from_bits(amax);
+    const bool live = __builtin_isfinite(sc);
+    const float yr = 1.0f / sc;
+    if (part == 0 && tid == 0) s[row] = sc;
+    int8_t* qr = q + (int64_t)row * ldq;
+    const int c0 = part * per, c1 = min(cpr, c0 + per);
+#pragma unroll
+    for (int j = 0; j < CH; j++) {
+        const int c = c0 + j * kThreads + tid;
+        if (c < c1) *reinterpret_cast<uint2*>(qr + 8 * c) = fni8::quant_chunk(a[j], sc, yr, live);
     }
 }
 
@@ -391,14 +488,35 @@ bool act_quant_vec_launch(int ch, const uint16_t* x, int64_t ldx, int64_t M, int
 
 // Rows per launch below which a row gets a 1024-thread workgroup.
 constexpr int64_t kFewRows = 256;
+// Rows per launch up to which, given a workspace, G workgroups share a row
+// (G = the row's 16-byte chunks over 256 threads x kSplitChunks, 2..8).
+constexpr int64_t kSplitRows = 128;
+constexpr int kSplitChunks = 1;
+constexpr int kSplitMaxParts = 8;
+
+int act_quant_parts(int64_t M, int64_t I) {
+    if (M < 1 || M > kSplitRows || I % 8 != 0) return 0;
+    const int64_t per_wg = (int64_t)kThreads * kSplitChunks;
+    const int64_t g = (I / 8 + per_wg - 1) / per_wg;
+    return g >= 2 && g <= kSplitMaxParts ? (int)g : 0;
+}
 
 template <int ACT>
 int act_quant_launch(const uint16_t* x, int64_t ldx, int64_t M, int64_t I, int8_t* q,
-                     int64_t ldq, float* s, hipStream_t st) {
+                     int64_t ldq, float* s, uint64_t* work, int64_t work_bytes,
+                     hipStream_t st) {
     const bool vec = I % 8 == 0 && ldx % 8 == 0 && ldq % 8 == 0 && al16(x) &&
                      ((uintptr_t)q % 8) == 0;
     bool done = false;
-    if (vec && M < kFewRows)
+    const int G = act_quant_parts(M, I);
+    if (vec && G > 0 && work != nullptr &&
+        work_bytes >= fni8h::act_quant_workspace_bytes(M, I) && ((uintptr_t)work % 256) == 0) {
+        const unsigned grid = (unsigned)(((M + 7) / 8) * 8 * G);
+        hipLaunchKernelGGL((act_quant_split_kernel<ACT, kSplitChunks>), dim3(grid),
+                           dim3(kThreads), 0, st, x, ldx, (int)M, (int)I, G, q, ldq, s, work,
+                           fni8h::xcd_wait_ticks());
+        done = true;
+    } else if (vec && M < kFewRows)
         done = act_quant_vec_launch<ACT, 1024>(chunks_per_lane(I, 1024), x, ldx, M, I, q, ldq,
                                                s, st);
     else if (vec)
@@ -453,12 +571,20 @@ int launch_act_and_mul(const uint16_t* x, int64_t ldx, int64_t M, int64_t I, int
                                 : act_mul_launch<FNI8_ACT_GELU_TANH>(x, ldx, M, I, out, ldo, st);
 }
 
+int64_t act_quant_workspace_bytes(int64_t M, int64_t I) {
+    const int G = act_quant_parts(M, I);
+    if (G == 0) return 0;
+    return (int64_t)8 * ((M + 7) / 8 * 8) * G * kSplitLine * 8;
+}
+
 int launch_act_and_mul_quant(const uint16_t* x, int64_t ldx, int64_t M, int64_t I, int act,
-                             int8_t* q, int64_t ldq, float* s, hipStream_t st) {
+                             int8_t* q, int64_t ldq, float* s, int8_t* work, int64_t work_bytes,
+                             hipStream_t st) {
     if (M == 0) return FNI8_OK;
+    uint64_t* w = reinterpret_cast<uint64_t*>(work);
     return act == FNI8_ACT_SILU
-               ? act_quant_launch<FNI8_ACT_SILU>(x, ldx, M, I, q, ldq, s, st)
-               : act_quant_launch<FNI8_ACT_GELU_TANH>(x, ldx, M, I, q, ldq, s, st);
+               ? act_quant_launch<FNI8_ACT_SILU>(x, ldx, M, I, q, ldq, s, w, work_bytes, st)
+               : act_quant_launch<FNI8_ACT_GELU_TANH>(x, ldx, M, I, q, ldq, s, w, work_bytes, st);
 }
 
 int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* res, int64_t ldr,

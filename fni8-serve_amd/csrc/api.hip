@@ -567,7 +567,33 @@ int fni8_act_and_mul_quant_f16(const void* x, int64_t ldx, int64_t M, int64_t I,
     int rc = check_device();
     if (rc) return rc;
     return fni8h::launch_act_and_mul_quant((const uint16_t*)x, ldx, M, I, act, xq, ldq, xs,
-                                           (hipStream_t)stream);
+                                           nullptr, 0, (hipStream_t)stream);
+}
+
+int fni8_act_and_mul_quant_f16_ws(const void* x, int64_t ldx, int64_t M, int64_t I, int act,
+                                  int8_t* xq, int64_t ldq, float* xs, void* workspace,
+                                  int64_t workspace_bytes, void* stream) {
+    fni8h::g_detail[0] = 0;
+    REQUIRE(x && xq && xs, FNI8_ERR_NULL, "x, xq and xs are required");
+    REQUIRE(M >= 0 && M < kMaxDim && I > 0 && I < kMaxDim / 2 && I % 4 == 0, FNI8_ERR_SHAPE,
+            "M=%lld I=%lld out of range (I a multiple of 4)", (long long)M, (long long)I);
+    REQUIRE(act == FNI8_ACT_SILU || act == FNI8_ACT_GELU_TANH, FNI8_ERR_SHAPE,
+            "unknown activation %d", act);
+    REQUIRE(ldx >= 2 * I && ldq >= I, FNI8_ERR_STRIDE, "ldx=%lld < 2I or ldq=%lld < I",
+            (long long)ldx, (long long)ldq);
+    REQUIRE(aligned(x, 2) && aligned(xs, 4), FNI8_ERR_ALIGN, "x or xs misaligned");
+    REQUIRE(workspace_bytes >= 0 && (!workspace || aligned(workspace, 256)), FNI8_ERR_ALIGN,
+            "workspace must be 256-byte aligned with a size >= 0");
+    int rc = check_device();
+    if (rc) return rc;
+    return fni8h::launch_act_and_mul_quant((const uint16_t*)x, ldx, M, I, act, xq, ldq, xs,
+                                           static_cast<int8_t*>(workspace),
+                                           workspace ? workspace_bytes : 0, (hipStream_t)stream);
+}
+
+int64_t fni8_act_and_mul_quant_workspace_bytes(int64_t M, int64_t I) {
+    if (M < 0 || I <= 0 || M >= kMaxDim || I >= kMaxDim / 2) return 0;
+    return fni8h::act_quant_workspace_bytes(M, I);
 }
 
 int fni8_rmsnorm_f16(const void* x, int64_t ldx, const void* residual, int64_t ldr,

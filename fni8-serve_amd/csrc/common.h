@@ -440,8 +440,12 @@ int launch_moe_combine(const uint16_t* yr, int64_t H, const int32_t* topi,
                        uint16_t* out, hipStream_t st);
 int launch_act_and_mul(const uint16_t* x, int64_t ldx, int64_t M, int64_t I, int act,
                        uint16_t* out, int64_t ldo, hipStream_t st);
+// With a workspace of act_quant_workspace_bytes(M, I) bytes (256-byte aligned),
+// few rows are split over several workgroups each; NULL = one workgroup a row.
 int launch_act_and_mul_quant(const uint16_t* x, int64_t ldx, int64_t M, int64_t I, int act,
-                             int8_t* q, int64_t ldq, float* s, hipStream_t st);
+                             int8_t* q, int64_t ldq, float* s, int8_t* work, int64_t work_bytes,
+                             hipStream_t st);
+int64_t act_quant_workspace_bytes(int64_t M, int64_t I);
 // RMSNorm; with q non-NULL the normed row is quantized into q/s instead of
 // being written to out.  res_out receives x + res (only with res).
 int launch_rmsnorm(const uint16_t* x, int64_t ldx, const uint16_t* res, int64_t ldr,

@@ -404,9 +404,13 @@ def act_and_mul_quant(x: torch.Tensor, act: str = "silu"):
     xq = torch.empty((M, I), dtype=torch.int8, device=dev)
     xs = torch.empty((M,), dtype=torch.float32, device=dev)
     if M:
+        # few rows: several workgroups share a row and exchange partial maxima
+        # through a workspace (caching allocator; contents never matter)
+        nw = int(_lib.load().fni8_act_and_mul_quant_workspace_bytes(M, I))
+        work = torch.empty(nw, dtype=torch.uint8, device=dev) if nw else None
         with torch.cuda.device(dev):
-            _lib.call("fni8_act_and_mul_quant_f16", _ptr(x2), ldx, M, I, code, _ptr(xq), I,
-                      _ptr(xs), _stream(dev))
+            _lib.call("fni8_act_and_mul_quant_f16_ws", _ptr(x2), ldx, M, I, code, _ptr(xq), I,
+                      _ptr(xs), _ptr(work), nw, _stream(dev))
     return xq, xs
 
 

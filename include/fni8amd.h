@@ -368,6 +368,28 @@ int fni8_act_and_mul_quant_f16(const void* x, int64_t ldx, int64_t M, int64_t I,
                                int8_t* xq, int64_t ldq, float* xs, void* stream);
 
 /*
+ * fni8_act_and_mul_quant_f16 with a workspace (same arithmetic and outputs, bit
+ * for bit; replaces the same step, fni8serve/layers/mlp.py:39-40 -> linear.py:69).
+ * For few rows (M <= 128) several workgroups share a row,
+ * each activating a part of it, and exchange their partial row maxima through
+ * `workspace` inside one XCD (a part that does not arrive in time is recomputed,
+ * so the bits never depend on it).
+ *   workspace  device memory, 256-byte aligned, at least
+ *              fni8_act_and_mul_quant_workspace_bytes(M, I) bytes; any contents;
+ *              NULL or too small = one workgroup per row.  One per stream.
+ */
+int fni8_act_and_mul_quant_f16_ws(const void* x, int64_t ldx, int64_t M, int64_t I, int act,
+                                  int8_t* xq, int64_t ldq, float* xs, void* workspace,
+                                  int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes of fni8_act_and_mul_quant_f16_ws: 8 * (M rounded up to 8) *
+ * G * 128, G = ceil(I / 2048) parts per row where 2 <= G <= 8 and M <= 128,
+ * else 0 (e.g. 393,216 for M = 64, I = 12288).
+ */
+int64_t fni8_act_and_mul_quant_workspace_bytes(int64_t M, int64_t I);
+
+/*
  * RMSNorm: `fni8.rmsnorm(x, weight, eps, residual=, unit_offset=)` (replaces
  * fni8serve/layers/norm.py:51-52; semantics of its eager form norm.py:37-58).
  *   h = residual ? fp16(x + residual) : x

@@ -183,6 +183,28 @@ def test_split_k_workspace_size_and_argument_checks(lib):
     assert rc == -1
 
 
+def test_act_quant_workspace_size_and_argument_checks(lib):
+    """fni8_act_and_mul_quant_f16_ws: 8 XCD regions of (M rounded up to 8) * G
+    128-byte lines for G = ceil(I / 2048) parts per row, 2 <= G <= 8 and
+    M <= 128; none otherwise (one workgroup per row).  A misaligned workspace
+    is an argument error raised before any launch."""
+    for M, I in ((1, 12288), (64, 12288), (128, 12288), (33, 4112), (9, 3072), (5, 16384)):
+        G = -(-I // 2048)
+        assert lib.fni8_act_and_mul_quant_workspace_bytes(M, I) == 8 * (-(-M // 8) * 8) * G * 128
+    assert lib.fni8_act_and_mul_quant_workspace_bytes(64, 12288) == 393216
+    for M, I in ((0, 12288), (129, 12288), (4096, 12288), (16, 768), (16, 2048), (4, 1004),
+                 (2, 16392), (2, 40000)):
+        assert lib.fni8_act_and_mul_quant_workspace_bytes(M, I) == 0, (M, I)
+    P = ctypes.c_void_p
+    fake = P(0x1000)
+    rc = lib.fni8_act_and_mul_quant_f16_ws(fake, 24576, 4, 12288, 0, fake, 12288, fake,
+                                           P(0x1080), 1 << 20, None)
+    assert rc == -3 and b"workspace" in lib.fni8_last_error()
+    rc = lib.fni8_act_and_mul_quant_f16_ws(fake, 24576, 4, 12288, 7, fake, 12288, fake, fake,
+                                           1 << 20, None)
+    assert rc == -2
+
+
 def test_workspace_size_and_argument_checks(lib):
     """The one-launch path's workspace: 8 regions of (2304 + M*K rounded up to
     256) bytes for the shapes it takes (5..16 tokens on QKV- and down-shaped

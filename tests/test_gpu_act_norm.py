@@ -65,6 +65,53 @@ def test_act_and_mul_quant_bitexact(pkg, act, M, I):
     assert _same_f32(xs.cpu().numpy(), s)
 
 
+@pytest.mark.parametrize("act", ["silu", "gelu_tanh"])
+@pytest.mark.parametrize("M,I", [(1, 12288), (5, 12288), (64, 12288), (128, 12288), (33, 4112),
+                                 (9, 3072)])
+def test_act_quant_split_rows(pkg, act, M, I):
+    """fni8_act_and_mul_quant_f16_ws for few rows: G workgroups share each row and
+    exchange partial maxima through the workspace.  Against the oracle, bit for
+    bit, on a zeroed workspace (then exactly one XCD region holds each part's
+    flag: the split kernel ran), on a workspace of garbage, and with the wait
+    bound at 0 (parts whose flag is not there at the first look are
+    recomputed).  I = 4112 leaves the last part of a row shorter."""
+    import ctypes
+    from importlib import import_module
+    lib = import_module("fni8serve_amd._lib")
+    raw = lib.load()
+    nw = int(raw.fni8_act_and_mul_quant_workspace_bytes(M, I))
+    G = -(-I // 2048)
+    assert nw == 8 * (-(-M // 8) * 8) * G * 128 and 2 <= G <= 8, (nw, G)
+    x = _merged(M, I, seed=M * 13 + I, specials=(M % 2 == 1))
+    q_ref, s_ref = o.act_and_mul_quant_f16(x, act)
+    xd = torch.from_numpy(x).cuda()
+    code = 0 if act == "silu" else 1
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    mpad = -(-M // 8) * 8
+    for case in ("zeroed", "stale", "recompute"):
+        if case == "zeroed":
+            work = torch.zeros(nw, dtype=torch.uint8, device="cuda")
+        else:
+            work = torch.randint(0, 256, (nw,), dtype=torch.uint8,
+                                 generator=torch.Generator().manual_seed(M)).cuda()
+        xq = torch.empty((M, I), dtype=torch.int8, device="cuda")
+        xs = torch.empty((M,), dtype=torch.float32, device="cuda")
+        if case == "recompute":
+            raw.fni8_debug_coop_wait_ticks(0)
+        try:
+            lib.call("fni8_act_and_mul_quant_f16_ws", ctypes.c_void_p(xd.data_ptr()), 2 * I, M,
+                     I, code, ctypes.c_void_p(xq.data_ptr()), I, ctypes.c_void_p(xs.data_ptr()),
+                     ctypes.c_void_p(work.data_ptr()), nw, st)
+            torch.cuda.synchronize()
+        finally:
+            raw.fni8_debug_coop_wait_ticks(-1)
+        assert np.array_equal(xq.cpu().numpy(), q_ref), case
+        assert _same_f32(xs.cpu().numpy(), s_ref), case
+        if case == "zeroed":
+            flags = work.view(torch.int64).view(8, mpad, G, 16)[:, :M, :, 0].cpu().numpy()
+            assert np.all((flags != 0).sum(axis=0) == 1), "one flag per (row, part)"
+
+
 def test_act_kernels_full_size_prefill(pkg):
     """Qwen3-8B gate_up output at M = 2048 (100 MB): both kernels against the
     oracle, and the fused form against quantize_rowwise of the unfused one."""
