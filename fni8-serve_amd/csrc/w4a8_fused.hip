@@ -233,7 +233,7 @@ __global__ __launch_bounds__(WAVES * 64) void w4a8_mfma_fused_kernel(
 
 #pragma unroll 1
     for (int rd = 0; rd < NR; rd++) {
-        if (rd > 0 && rd + 1 < NR) load(wb, rd + 1);  // round 1 is already in flight
+        if (rd > 0 && rd + 1 < NR) load(wb, rd + 1);  // rd = 1 is already in flight
 #pragma unroll
         for (int b = 0; b < NB; b++)
 #pragma unroll
