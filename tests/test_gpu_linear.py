@@ -75,6 +75,18 @@ def test_cpu_case_bitexact(pkg, wl, cuda):
     _check_full(pkg, x, q, s, tag="qwen3-0.6b gate_up M=8")
 
 
+@pytest.mark.parametrize("N,K", [(768, 2048), (16384, 512), (256, 12288)])
+def test_decode_every_token_count_bitexact(pkg, wl, cuda, N, K):
+    """Every token count from 1 to 64 through linear(): the fused-quantization
+    kernels up to 4 tokens, the one- or two-launch paths up to 16, the MFMA
+    GEMM's 16-, 32- and 64-token blocks above, on a generic, a wide (N >= 16384)
+    and a long-K shape; every intermediate bit for bit against the oracle."""
+    q, s = wl.weight_i8(N, K, seed=N + K)
+    for M in range(1, 65):
+        x = wl.activations(M, K, seed=31 * M + K)
+        _check_full(pkg, x, q, s, tag=f"M={M} N={N} K={K}")
+
+
 @pytest.mark.parametrize("M,N,K", [
     (3, 100, 256), (17, 48, 512), (33, 4096, 4096), (65, 256, 1024), (100, 640, 2048),
     (257, 384, 1024), (130, 130, 128), (8, 16, 64), (64, 1000, 192),
