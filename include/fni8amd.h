@@ -13,8 +13,9 @@
  *     `stream`; nothing synchronises the host.
  *   - The library allocates no device memory; every buffer comes from the
  *     caller, so calls can be captured in a HIP graph.  Calls are reentrant.
- *     The one piece of mutable global state is the per-GPU scratch of
- *     fni8_linear_w8a8_f16_noalloc (below), which only that entry point uses.
+ *     Mutable global state: the per-GPU scratch of
+ *     fni8_linear_w8a8_f16_noalloc (below), which only that entry point uses,
+ *     and the process-wide settings of the fni8_debug_* test hooks.
  *   - fp16 tensors are IEEE binary16 passed as `void*` / `uint16_t*`.
  *   - Weights follow the per_row_i8 QTensor layout (models/weights.py:18-25):
  *     data int8 [N, K] row-major (K contiguous), scale fp32 [N].
